@@ -1,0 +1,50 @@
+// moe_layer.h -- one mixture-of-experts FFN layer driven through the qmatvec / gpu_ops C ABI.
+//
+// The caller side of the path: the launch sequence of the reference's QwenModel::moe_core and moe_core_one
+// (src/qwen_model.cpp:864-937), as a C entry point so that a harness (or the engine's forward pass) can run a
+// whole layer with one call. Router logits (F32 matvec, or given), moe_router, then:
+//   T == 1: the experts' gate/up in one launch (the shared expert as one more slot, id -1, when it has the
+//           experts' width and type), SwiGLU quantized for down, down, moe_combine;
+//   T 2..7: the same per token (each token's experts read once per token);
+//   T >= 8: gpu_moe_group, the grouped gate / up / down on the expert tiles, the shared expert dense, combine.
+// All buffers are device memory; scratch is caller-owned (moe_layer_scratch_bytes). Asynchronous on `stream`.
+
+#ifndef MOE_LAYER_H
+#define MOE_LAYER_H
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct moe_layer_desc {
+    int type;          // expert weight type (gate, up and down share it): 8, 12, 100 or 101
+    int n_embd;        // E
+    int n_expert;      // NE
+    int n_used;        // NU
+    int n_ff;          // FE (the shared expert, when present, has the same width)
+    const float* w_router;   // [NE][E] F32
+    const void* w_gate;      // [NE * FE] native rows of qt_row_size(type, E)
+    const void* w_up;
+    const void* w_down;      // [NE * E] native rows of qt_row_size(type, FE)
+    const void* s_gate;      // shared expert [FE] rows, or NULL
+    const void* s_up;
+    const void* s_down;      // [E] rows
+    const float* w_shexp;    // [E] sigmoid gate of the shared expert, or NULL (gate 1)
+} moe_layer_desc;
+
+// Device bytes of scratch a call with up to max_t tokens needs
+size_t moe_layer_scratch_bytes(const moe_layer_desc* d, int max_t);
+
+// out [T][E] = MoE(x [T][E]); logits [T][NE] (NULL: W_router x). ids_out [T][NU] / wts_out [T][NU] (optional,
+// NULL) receive the routing. scratch: moe_layer_scratch_bytes(d, >= T) bytes, 256-byte aligned.
+hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x, const float* logits, int T, float* out,
+                             int* ids_out, float* wts_out, void* scratch, size_t scratch_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif  // MOE_LAYER_H

@@ -1,0 +1,8 @@
+// ref_shim.cpp -- C-linkage wrappers around the reference's own CPU ops, so that the tests can call the
+// reference build in oracle/_ref (src/qwen_ops.h declares them with C++ linkage). Test infrastructure only.
+#include "qwen_ops.h"
+
+extern "C" {
+void ref_rmsnorm(const float* x, const float* w, float* y, int n, float eps) { qwen_rmsnorm(x, w, y, n, eps); }
+float ref_silu(float x) { return qwen_silu(x); }
+}

@@ -1,0 +1,533 @@
+// expert_matvec.hip -- decode expert matvecs (and the dense / per-entry variants) on gfx950, wave64, plus the
+// split-plane weight registry and the C-ABI launchers of the int8 path.
+//
+// Kernel shape: a workgroup of four waves; in a wave, groups of L lanes (L in {8, 16, 32, 64}) each own one
+// weight row at a time and R rows in flight (the R rows' loads are issued together). Lane gl of a group takes
+// the row's units gl, gl + L, ...; the group then sums its lanes. Each unit's integer dot is exact; the float
+// terms are added per lane and then by an xor tree over the group.
+//
+// Expert indirection (src/matvec_q.hip:1905-1933): slot j of token t uses expert e = ids[t * n_used + j] (rows
+// e * N .. of W), input row t (x_per_slot 0) or t * n_used + j (1), output row t * n_used + j; grid.y >=
+// n_used selects the second matrix (W2 -> y2); e = -1 selects the extra matrix Wx / W2x.
+
+#include <map>
+#include <mutex>
+
+#include "expert_units.h"
+#include "host_common.h"
+#include "qmatvec.h"
+
+struct MvArgs {
+    const uint8_t* v[4];  // W, W2, Wx, W2x: native rows, or the value planes of their split-plane copies
+    const uint8_t* s[4];  // scale planes (split-plane only)
+    long long vrb, srb;   // bytes per row in the value / scale plane (native: row_bytes, 0)
+    const int* ids;       // nullptr: dense (no expert choice)
+    int n_used, x_per_slot;
+    const int8_t* xq;  // activations: int8 values, scales, Q8_K sums
+    const float* xd;
+    const int* xbs;
+    float* y;
+    float* y2;
+    long long ldy;  // output row stride (id mode: N)
+    int N, N2, K;
+};
+
+template <int TYPE, bool PACKED>
+__device__ __forceinline__ void load_unit(const uint8_t* vrow, const uint8_t* srow, int u, int nu, WUnit<TYPE>& w) {
+    if constexpr (PACKED)
+        load_packed<TYPE>(vrow, srow, u, nu, w);
+    else
+        load_native<TYPE>(vrow, u, w);
+}
+
+// R rows (row0 + r * stride) of the matrix at (vbase, sbase) against one input row; returns the group sums
+template <int TYPE, bool PACKED, int L, int R>
+__device__ __forceinline__ void rows_dot(const uint8_t* vbase, const uint8_t* sbase, long long vrb, long long srb,
+                                         int row0, int stride, int nrows, const int8_t* xq, const float* xd,
+                                         const int* xbs, int K, int gl, float acc[R]) {
+    const int nu = fmt_units(TYPE, K);
+    const uint8_t* vr[R];
+    const uint8_t* sr[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r * stride, nrows - 1);  // rows past the end load a valid row, unused
+        vr[r] = vbase + (long long)row * vrb;
+        sr[r] = PACKED ? sbase + (long long)row * srb : nullptr;
+        acc[r] = 0.0f;
+    }
+    for (int u = gl; u < nu; u += L) {
+        XUnit<TYPE> x;
+        load_x<TYPE>(xq, xd, xbs, u, x);
+        WUnit<TYPE> w[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) load_unit<TYPE, PACKED>(vr[r], sr[r], u, nu, w[r]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] += term<TYPE>(w[r], x, u);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = group_sum<L>(acc[r]);
+}
+
+template <int TYPE>
+__device__ __forceinline__ void act_row(const MvArgs& a, long long in_row, const int8_t*& xq, const float*& xd,
+                                        const int*& xbs) {
+    xq = a.xq + in_row * a.K;
+    xd = a.xd + in_row * (a.K / (Fmt<TYPE>::Q8K ? 256 : 32));
+    xbs = Fmt<TYPE>::Q8K ? a.xbs + in_row * (a.K / 16) : nullptr;
+}
+
+// grid (row blocks, n_used * (1 or 2) slots, T tokens) in id mode; (row blocks, 1 or 2 matrices, T) dense
+template <int TYPE, bool PACKED, int L, int R>
+__global__ void __launch_bounds__(256) k_expert_mv(MvArgs a) {
+    constexpr int G = 64 / L;  // row groups per wave
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int gl = lane & (L - 1), grp = lane / L;
+    const int row0 = (blockIdx.x * 4 + wv) * (R * G) + grp;
+    const int t = blockIdx.z;
+    int slot, mi, e;
+    long long out_row;
+    if (a.ids) {
+        const bool m2 = (int)blockIdx.y >= a.n_used;
+        slot = blockIdx.y - (m2 ? a.n_used : 0);
+        e = a.ids[(long long)t * a.n_used + slot];
+        mi = (e >= 0 ? 0 : 2) + (m2 ? 1 : 0);
+        out_row = (long long)t * a.n_used + slot;
+    } else {
+        slot = 0;
+        e = 0;
+        mi = blockIdx.y;
+        out_row = t;
+    }
+    const int nrows = mi & 1 ? a.N2 : a.N;
+    if (row0 - grp >= nrows) return;  // the whole wave is past the end (uniform per wave)
+    const long long rbase = e >= 0 ? (long long)e * nrows : 0;
+    const uint8_t* vbase = a.v[mi] + rbase * a.vrb;
+    const uint8_t* sbase = PACKED ? a.s[mi] + rbase * a.srb : nullptr;
+    const long long in_row = a.ids && a.x_per_slot ? (long long)t * a.n_used + slot : t;
+    const int8_t* xq;
+    const float* xd;
+    const int* xbs;
+    act_row<TYPE>(a, in_row, xq, xd, xbs);
+    float acc[R];
+    rows_dot<TYPE, PACKED, L, R>(vbase, sbase, a.vrb, a.srb, row0, G, nrows, xq, xd, xbs, a.K, gl, acc);
+    if (gl == 0) {
+        float* y = (mi & 1 ? a.y2 : a.y) + out_row * a.ldy;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + r * G < nrows) y[row0 + r * G] = acc[r];
+    }
+}
+
+// Prefill per-entry kernel on gpu_moe_group's tiles: grid (row blocks, max_tiles). Each entry of the tile gets
+// the sum the decode kernel would give it (the weights are re-read per entry from L2).
+template <int TYPE, bool PACKED, int L, int R>
+__global__ void __launch_bounds__(256) k_expert_entries(MvArgs a, const int* n_tiles, const int* tile_e,
+                                                        const int* tile_start, const int* tile_n, const int* in_rows,
+                                                        const int* out_rows) {
+    constexpr int G = 64 / L;
+    const int k = blockIdx.y;
+    if (k >= *n_tiles) return;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int gl = lane & (L - 1), grp = lane / L;
+    const int row0 = (blockIdx.x * 4 + wv) * (R * G) + grp;
+    if (row0 - grp >= a.N) return;
+    const long long rbase = (long long)tile_e[k] * a.N;
+    const uint8_t* vbase = a.v[0] + rbase * a.vrb;
+    const uint8_t* sbase = PACKED ? a.s[0] + rbase * a.srb : nullptr;
+    const int st = tile_start[k], cnt = tile_n[k];
+    for (int i = 0; i < cnt; ++i) {
+        const int8_t* xq;
+        const float* xd;
+        const int* xbs;
+        act_row<TYPE>(a, in_rows[st + i], xq, xd, xbs);
+        float acc[R];
+        rows_dot<TYPE, PACKED, L, R>(vbase, sbase, a.vrb, a.srb, row0, G, a.N, xq, xd, xbs, a.K, gl, acc);
+        if (gl == 0) {
+            float* y = a.y + (long long)out_rows[st + i] * a.N;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (row0 + r * G < a.N) y[row0 + r * G] = acc[r];
+        }
+    }
+}
+
+// ------------------------------------------------------------------ split-plane copies
+
+// One thread per native block (32 values; 256 for Q4_K)
+template <int TYPE>
+__global__ void __launch_bounds__(256) k_pack(const uint8_t* W, long long row_bytes, long long rows, int K, uint8_t* V,
+                                              uint8_t* S) {
+    constexpr int BV = TYPE == QT_Q4_K ? 256 : 32, BB = Fmt<TYPE>::BLOCK_BYTES;
+    const int nb = K / BV;
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * nb) return;
+    const long long r = i / nb;
+    const int b = (int)(i - r * nb);
+    const uint8_t* src = W + r * row_bytes + (long long)b * BB;
+    uint8_t* vr = V + r * fmt_value_row(TYPE, K);
+    uint8_t* sr = S + r * fmt_scale_row(TYPE, K);
+    if constexpr (TYPE == QT_Q8_0) {
+        sr[2 * b] = src[0];
+        sr[2 * b + 1] = src[1];
+        for (int j = 0; j < 16; ++j) {
+            vr[16 * b + j] = src[2 + j];
+            vr[16 * (nb + b) + j] = src[18 + j];
+        }
+    } else if constexpr (TYPE == QT_ROCMFP4) {
+        for (int j = 0; j < 16; ++j) vr[16 * b + j] = src[j];
+        sr[2 * b] = src[16];
+        sr[2 * b + 1] = src[17];
+    } else if constexpr (TYPE == QT_ROCMFP4_FAST) {
+        for (int j = 0; j < 16; ++j) vr[16 * b + j] = src[j];
+        sr[b] = src[16];
+    } else {  // Q4_K: head -> scale plane, chunk c (32 value bytes) -> unit 4b + c in the two half planes
+        const int nu = K / 64;
+        for (int j = 0; j < 16; ++j) sr[16 * b + j] = src[j];
+        for (int c = 0; c < 4; ++c) {
+            const int u = 4 * b + c;
+            for (int j = 0; j < 16; ++j) {
+                vr[16 * u + j] = src[16 + 32 * c + j];
+                vr[16 * (nu + u) + j] = src[16 + 32 * c + 16 + j];
+            }
+        }
+    }
+}
+
+namespace {
+
+struct Packed {
+    uintptr_t end;
+    int type, K;
+    size_t row_bytes;
+    long long rows;
+    uint8_t* mem;  // value plane, then scale plane
+};
+
+std::mutex g_pack_mu;
+std::map<uintptr_t, Packed> g_packed;  // keyed by the native W's start address
+
+size_t native_row(int type, int K) {
+    switch (type) {
+    case QT_Q8_0: return K % 32 ? 0 : (size_t)K / 32 * 34;
+    case QT_ROCMFP4: return K % 32 ? 0 : (size_t)K / 32 * 18;
+    case QT_ROCMFP4_FAST: return K % 32 ? 0 : (size_t)K / 32 * 17;
+    case QT_Q4_K: return K % 256 ? 0 : (size_t)K / 256 * 144;
+    default: return 0;
+    }
+}
+
+// The split-plane copy covering the native row pointer W (value and scale rows), or false
+bool find_packed(const void* W, int type, int K, size_t row_bytes, const uint8_t** v, const uint8_t** s) {
+    if (!W) return false;
+    std::lock_guard<std::mutex> lk(g_pack_mu);
+    auto it = g_packed.upper_bound((uintptr_t)W);
+    if (it == g_packed.begin()) return false;
+    --it;
+    const Packed& p = it->second;
+    const uintptr_t off = (uintptr_t)W - it->first;
+    if ((uintptr_t)W >= p.end || p.type != type || p.K != K || p.row_bytes != row_bytes || off % row_bytes) return false;
+    const long long row = (long long)(off / row_bytes);
+    *v = p.mem + row * fmt_value_row(type, K);
+    *s = p.mem + (size_t)p.rows * fmt_value_row(type, K) + row * fmt_scale_row(type, K);
+    return true;
+}
+
+int lanes_for(int type, int K) {
+    const int nu = fmt_units(type, K);
+    int L = 64;
+    while (L > 8 && (L > nu || nu % L != 0)) L /= 2;
+    return L;
+}
+
+constexpr int rows_in_flight(int L) { return L == 64 ? 4 : 2; }
+int rows_per_block(int L) { return 4 * rows_in_flight(L) * (64 / L); }
+
+template <int TYPE, bool PACKED>
+hipError_t launch_mv_t(const MvArgs& a, dim3 grid_yz, int L, int nrows, hipStream_t st) {
+    const dim3 g((nrows + rows_per_block(L) - 1) / rows_per_block(L), grid_yz.y, grid_yz.z), b(256);
+    switch (L) {
+    case 64: return launch_kernel(k_expert_mv<TYPE, PACKED, 64, rows_in_flight(64)>, g, b, 0, st, a);
+    case 32: return launch_kernel(k_expert_mv<TYPE, PACKED, 32, rows_in_flight(32)>, g, b, 0, st, a);
+    case 16: return launch_kernel(k_expert_mv<TYPE, PACKED, 16, rows_in_flight(16)>, g, b, 0, st, a);
+    default: return launch_kernel(k_expert_mv<TYPE, PACKED, 8, rows_in_flight(8)>, g, b, 0, st, a);
+    }
+}
+
+template <int TYPE, bool PACKED>
+hipError_t launch_entries_t(const MvArgs& a, int max_tiles, int L, const int32_t* n_tiles, const int32_t* tile_e,
+                            const int32_t* tile_start, const int32_t* tile_n, const int32_t* in_rows,
+                            const int32_t* out_rows, hipStream_t st) {
+    const dim3 g((a.N + rows_per_block(L) - 1) / rows_per_block(L), max_tiles), b(256);
+#define ENTRIES_CASE(LL)                                                                                          \
+    return launch_kernel(k_expert_entries<TYPE, PACKED, LL, rows_in_flight(LL)>, g, b, 0, st, a, n_tiles, tile_e, \
+                         tile_start, tile_n, in_rows, out_rows)
+    switch (L) {
+    case 64: ENTRIES_CASE(64);
+    case 32: ENTRIES_CASE(32);
+    case 16: ENTRIES_CASE(16);
+    default: ENTRIES_CASE(8);
+    }
+#undef ENTRIES_CASE
+}
+
+hipError_t launch_mv(int type, bool packed, const MvArgs& a, dim3 yz, int L, int nrows, hipStream_t st) {
+    switch (type) {
+    case QT_Q8_0: return packed ? launch_mv_t<QT_Q8_0, true>(a, yz, L, nrows, st) : launch_mv_t<QT_Q8_0, false>(a, yz, L, nrows, st);
+    case QT_ROCMFP4: return packed ? launch_mv_t<QT_ROCMFP4, true>(a, yz, L, nrows, st) : launch_mv_t<QT_ROCMFP4, false>(a, yz, L, nrows, st);
+    case QT_ROCMFP4_FAST: return packed ? launch_mv_t<QT_ROCMFP4_FAST, true>(a, yz, L, nrows, st) : launch_mv_t<QT_ROCMFP4_FAST, false>(a, yz, L, nrows, st);
+    case QT_Q4_K: return packed ? launch_mv_t<QT_Q4_K, true>(a, yz, L, nrows, st) : launch_mv_t<QT_Q4_K, false>(a, yz, L, nrows, st);
+    }
+    return hipErrorInvalidDeviceFunction;
+}
+
+// Fill the weight side of a: every non-null matrix from its split-plane copy if all of them have one, else all
+// native. Returns whether the copies are used.
+bool bind_weights(MvArgs& a, int type, int K, size_t row_bytes, const void* const W[4]) {
+    const uint8_t* v[4] = {nullptr, nullptr, nullptr, nullptr};
+    const uint8_t* s[4] = {nullptr, nullptr, nullptr, nullptr};
+    bool all = true;
+    for (int i = 0; i < 4; ++i)
+        if (W[i] && !find_packed(W[i], type, K, row_bytes, &v[i], &s[i])) all = false;
+    for (int i = 0; i < 4; ++i) {
+        a.v[i] = all ? v[i] : (const uint8_t*)W[i];
+        a.s[i] = all ? s[i] : nullptr;
+    }
+    a.vrb = all ? fmt_value_row(type, K) : (long long)row_bytes;
+    a.srb = all ? fmt_scale_row(type, K) : 0;
+    return all;
+}
+
+void bind_acts(MvArgs& a, int type, const qmatvec_q8* q) {
+    const bool kq = type == QT_Q4_K;
+    a.xq = kq ? q->qK : q->q0;
+    a.xd = kq ? q->dK : q->d0;
+    a.xbs = kq ? q->bsK : nullptr;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ C ABI
+
+extern "C" int qmatvec_q8_supported(int type, int K) {
+    if (K <= 0) return 0;
+    switch (type) {
+    case QT_Q8_0:
+    case QT_ROCMFP4:
+    case QT_ROCMFP4_FAST: return K % 32 == 0;
+    case QT_Q4_K: return K % 256 == 0;
+    default: return 0;
+    }
+}
+
+extern "C" size_t qmatvec_packed_bytes(int type, long long rows, int K) {
+    const size_t rb = native_row(type, K);
+    return rows > 0 ? rb * (size_t)rows : 0;
+}
+
+template <int TYPE>
+static hipError_t launch_pack(const void* W, size_t rb, long long rows, int K, uint8_t* mem, hipStream_t st) {
+    constexpr int BV = TYPE == QT_Q4_K ? 256 : 32;
+    const long long n = rows * (K / BV);
+    uint8_t* V = mem;
+    uint8_t* S = mem + (size_t)rows * fmt_value_row(TYPE, K);
+    return launch_kernel(k_pack<TYPE>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const uint8_t*)W,
+                         (long long)rb, rows, K, V, S);
+}
+
+extern "C" hipError_t qmatvec_pack_weights(int type, const void* W, size_t row_bytes, long long rows, int K,
+                                           hipStream_t stream) {
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (!qmatvec_q8_supported(type, K)) return hipErrorInvalidDeviceFunction;
+    if (!W || rows <= 0 || row_bytes != native_row(type, K)) return hipErrorInvalidValue;
+    const size_t bytes = row_bytes * (size_t)rows;
+    {
+        std::lock_guard<std::mutex> lk(g_pack_mu);
+        auto it = g_packed.lower_bound((uintptr_t)W);
+        if (it != g_packed.end() && it->first < (uintptr_t)W + bytes) return hipErrorInvalidValue;  // overlap
+        if (it != g_packed.begin() && std::prev(it)->second.end > (uintptr_t)W) return hipErrorInvalidValue;
+    }
+    void* mem = nullptr;
+    hipError_t e = hipMalloc(&mem, bytes);
+    if (e != hipSuccess) return e;
+    switch (type) {
+    case QT_Q8_0: e = launch_pack<QT_Q8_0>(W, row_bytes, rows, K, (uint8_t*)mem, stream); break;
+    case QT_ROCMFP4: e = launch_pack<QT_ROCMFP4>(W, row_bytes, rows, K, (uint8_t*)mem, stream); break;
+    case QT_ROCMFP4_FAST: e = launch_pack<QT_ROCMFP4_FAST>(W, row_bytes, rows, K, (uint8_t*)mem, stream); break;
+    default: e = launch_pack<QT_Q4_K>(W, row_bytes, rows, K, (uint8_t*)mem, stream); break;
+    }
+    if (e != hipSuccess) {
+        (void)hipFree(mem);
+        return e;
+    }
+    std::lock_guard<std::mutex> lk(g_pack_mu);
+    g_packed[(uintptr_t)W] = Packed{(uintptr_t)W + bytes, type, K, row_bytes, rows, (uint8_t*)mem};
+    return hipSuccess;
+}
+
+extern "C" void qmatvec_unpack_weights(const void* W) {
+    uint8_t* mem = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_pack_mu);
+        auto it = g_packed.find((uintptr_t)W);
+        if (it == g_packed.end()) return;
+        mem = it->second.mem;
+        g_packed.erase(it);
+    }
+    // launches already queued on any stream may still read the copy
+    if (hipDeviceSynchronize() == hipSuccess) (void)hipFree(mem);
+}
+
+// Drop every registration (library teardown)
+void moe_unpack_all(void) {
+    std::map<uintptr_t, Packed> all;
+    {
+        std::lock_guard<std::mutex> lk(g_pack_mu);
+        all.swap(g_packed);
+    }
+    if (all.empty()) return;
+    (void)hipDeviceSynchronize();
+    for (auto& kv : all) (void)hipFree(kv.second.mem);
+}
+
+static hipError_t check_common(int type, const void* W, size_t row_bytes, const qmatvec_q8* q, int K,
+                               long long in_rows) {
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (!qmatvec_q8_supported(type, K)) return hipErrorInvalidDeviceFunction;
+    if (!W || !q || row_bytes != native_row(type, K) || (row_bytes & 3) || !aligned(W, 4) ||
+        in_rows * K > (long long)q->max_k)
+        return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+extern "C" hipError_t qmatvec_launch_q8_id_x(int type, const void* W, const void* W2, const void* Wx, const void* W2x,
+                                             size_t row_bytes, const int32_t* ids, int n_used, int x_per_slot,
+                                             const qmatvec_q8* q, float* y, float* y2, int N, int K, int T,
+                                             hipStream_t stream) {
+    if (T <= 0 || n_used <= 0 || N <= 0 || !ids || !y || (W2 && !y2)) return hipErrorInvalidValue;
+    const hipError_t c = check_common(type, W, row_bytes, q, K, (long long)T * (x_per_slot ? n_used : 1));
+    if (c != hipSuccess) return c;
+    if (!aligned(W2, 4) || !aligned(Wx, 4) || !aligned(W2x, 4)) return hipErrorInvalidValue;
+    MvArgs a = {};
+    const void* Ws[4] = {W, W2, Wx, W2 ? W2x : nullptr};
+    const bool packed = bind_weights(a, type, K, row_bytes, Ws);
+    bind_acts(a, type, q);
+    a.ids = ids;
+    a.n_used = n_used;
+    a.x_per_slot = x_per_slot ? 1 : 0;
+    a.y = y;
+    a.y2 = y2;
+    a.ldy = N;
+    a.N = a.N2 = N;
+    a.K = K;
+    const int L = lanes_for(type, K);
+    return launch_mv(type, packed, a, dim3(1, n_used * (W2 ? 2 : 1), T), L, N, stream);
+}
+
+extern "C" hipError_t qmatvec_launch_q8_id(int type, const void* W, size_t row_bytes, const int32_t* ids, int n_used,
+                                           int x_per_slot, const qmatvec_q8* q, float* y, int N, int K, int T,
+                                           hipStream_t stream) {
+    return qmatvec_launch_q8_id_x(type, W, nullptr, nullptr, nullptr, row_bytes, ids, n_used, x_per_slot, q, y,
+                                  nullptr, N, K, T, stream);
+}
+
+extern "C" hipError_t qmatvec_launch_q8_id_pair(int type, const void* W, const void* W2, size_t row_bytes,
+                                                const int32_t* ids, int n_used, int x_per_slot, const qmatvec_q8* q,
+                                                float* y, float* y2, int N, int K, int T, hipStream_t stream) {
+    if (!W2) return hipErrorInvalidValue;
+    return qmatvec_launch_q8_id_x(type, W, W2, nullptr, nullptr, row_bytes, ids, n_used, x_per_slot, q, y, y2, N, K,
+                                  T, stream);
+}
+
+static hipError_t dense(int type, const void* W, int N, float* y, const void* W2, int N2, float* y2,
+                        size_t row_bytes, const qmatvec_q8* q, int K, int T, long long ldy, hipStream_t stream) {
+    if (N <= 0 || T <= 0 || !y || (W2 && (N2 <= 0 || !y2)) || ldy < N) return hipErrorInvalidValue;
+    const hipError_t c = check_common(type, W, row_bytes, q, K, T);
+    if (c != hipSuccess) return c;
+    if (!aligned(W2, 4)) return hipErrorInvalidValue;
+    MvArgs a = {};
+    const void* Ws[4] = {W, W2, nullptr, nullptr};
+    const bool packed = bind_weights(a, type, K, row_bytes, Ws);
+    bind_acts(a, type, q);
+    a.ids = nullptr;
+    a.n_used = 1;
+    a.y = y;
+    a.y2 = y2;
+    a.ldy = ldy;
+    a.N = N;
+    a.N2 = W2 ? N2 : 0;
+    a.K = K;
+    return launch_mv(type, packed, a, dim3(1, W2 ? 2 : 1, T), lanes_for(type, K), W2 && N2 > N ? N2 : N, stream);
+}
+
+extern "C" hipError_t qmatvec_launch_q8_pair(int type, const void* W, int N, float* y, const void* W2, int N2,
+                                             float* y2, size_t row_bytes, const qmatvec_q8* q, int K,
+                                             hipStream_t stream) {
+    if (W2 && N2 > 0) {
+        if (N2 != N) return hipErrorInvalidValue;  // one output stride for both (the two row counts match)
+        return dense(type, W, N, y, W2, N2, y2, row_bytes, q, K, 1, N, stream);
+    }
+    return dense(type, W, N, y, nullptr, 0, nullptr, row_bytes, q, K, 1, N, stream);
+}
+
+extern "C" hipError_t qmatvec_launch_q8(int type, const void* W, size_t row_bytes, const qmatvec_q8* q, float* y,
+                                        int N, int K, hipStream_t stream) {
+    return dense(type, W, N, y, nullptr, 0, nullptr, row_bytes, q, K, 1, N, stream);
+}
+
+extern "C" hipError_t qmatvec_launch_q8_batch(int type, const void* W, size_t row_bytes, const qmatvec_q8* q, float* y,
+                                              long long ldy, int N, int K, int T, hipStream_t stream) {
+    return dense(type, W, N, y, nullptr, 0, nullptr, row_bytes, q, K, T, ldy, stream);
+}
+
+// Entry tiles of the per-entry kernel (MFMA tiles: see grouped_gemm.hip)
+#define ENTRY_TILE 64
+
+hipError_t moe_launch_entries(int type, const void* W, size_t row_bytes, const qmatvec_q8* q, float* y, int N, int K,
+                              int max_tiles, const int32_t* n_tiles, const int32_t* tile_e, const int32_t* tile_start,
+                              const int32_t* tile_n, const int32_t* in_rows, const int32_t* out_rows,
+                              hipStream_t stream) {
+    MvArgs a = {};
+    const void* Ws[4] = {W, nullptr, nullptr, nullptr};
+    const bool packed = bind_weights(a, type, K, row_bytes, Ws);
+    bind_acts(a, type, q);
+    a.N = a.N2 = N;
+    a.ldy = N;
+    a.K = K;
+    a.y = y;
+    const int L = lanes_for(type, K);
+#define ENT(TT)                                                                                                       \
+    return packed ? launch_entries_t<TT, true>(a, max_tiles, L, n_tiles, tile_e, tile_start, tile_n, in_rows,        \
+                                               out_rows, stream)                                                      \
+                  : launch_entries_t<TT, false>(a, max_tiles, L, n_tiles, tile_e, tile_start, tile_n, in_rows,       \
+                                                out_rows, stream)
+    switch (type) {
+    case QT_Q8_0: ENT(QT_Q8_0);
+    case QT_ROCMFP4: ENT(QT_ROCMFP4);
+    case QT_ROCMFP4_FAST: ENT(QT_ROCMFP4_FAST);
+    case QT_Q4_K: ENT(QT_Q4_K);
+    }
+#undef ENT
+    return hipErrorInvalidDeviceFunction;
+}
+
+extern "C" int qmatvec_id_batch_tile(int type, int N, int K) {
+    (void)N;
+    return qmatvec_q8_supported(type, K) ? ENTRY_TILE : 16;
+}
+
+extern "C" int qmatvec_q8_id_batch_supported(int type, int K) { return qmatvec_q8_supported(type, K); }
+
+extern "C" hipError_t qmatvec_launch_q8_id_batch(int type, const void* W, size_t row_bytes, const qmatvec_q8* q,
+                                                 float* y, int N, int K, int max_tiles, int tile,
+                                                 const int32_t* n_tiles, const int32_t* tile_e,
+                                                 const int32_t* tile_start, const int32_t* tile_n,
+                                                 const int32_t* in_rows, const int32_t* out_rows, hipStream_t stream) {
+    if (N <= 0 || max_tiles <= 0 || tile <= 0 || tile > qmatvec_id_batch_tile(type, N, K) || !y || !n_tiles ||
+        !tile_e || !tile_start || !tile_n || !in_rows || !out_rows)
+        return hipErrorInvalidValue;
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (!qmatvec_q8_supported(type, K)) return hipErrorInvalidDeviceFunction;
+    if (!W || !q || row_bytes != native_row(type, K) || !aligned(W, 4)) return hipErrorInvalidValue;
+    return moe_launch_entries(type, W, row_bytes, q, y, N, K, max_tiles, n_tiles, tile_e, tile_start, tile_n, in_rows,
+                              out_rows, stream);
+}

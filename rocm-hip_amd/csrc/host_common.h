@@ -1,0 +1,26 @@
+// host_common.h -- launch helper and library state shared by the C-ABI launchers.
+#ifndef HOST_COMMON_H
+#define HOST_COMMON_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+// 1 once qmatvec_init / gpu_ops_init found a gfx950 device (either one initialises the whole library)
+extern "C" int moe_lib_ready(void);
+
+template <typename T>
+struct same_type {
+    typedef T type;
+};
+
+// Launch a kernel and return its launch status (no sticky error state is consulted)
+template <typename... Args>
+static inline hipError_t launch_kernel(void (*k)(Args...), dim3 grid, dim3 block, size_t shm, hipStream_t s,
+                                       typename same_type<Args>::type... args) {
+    void* ptrs[] = {(void*)&args..., nullptr};
+    return hipLaunchKernel((const void*)k, grid, block, ptrs, shm, s);
+}
+
+static inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+#endif  // HOST_COMMON_H

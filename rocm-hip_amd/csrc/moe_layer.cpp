@@ -1,0 +1,171 @@
+// moe_layer.cpp -- moe_layer_forward: one MoE FFN layer as the reference's QwenModel::moe_core issues it
+// (src/qwen_model.cpp:864-937), through this library's C ABI only. See include/moe_layer.h.
+
+#include "moe_layer.h"
+
+#include <stdint.h>
+
+#include "gpu_ops.h"
+#include "qmatvec.h"
+
+namespace {
+
+size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
+int r256(long long k) { return (int)((k + 255) / 256 * 256); }
+
+size_t row_size(int type, int k) {
+    switch (type) {
+    case 8: return (size_t)k / 32 * 34;
+    case 100: return (size_t)k / 32 * 18;
+    case 101: return (size_t)k / 32 * 17;
+    case 12: return (size_t)k / 256 * 144;
+    }
+    return 0;
+}
+
+// Scratch carve-up; every piece 256-byte aligned
+struct Plan {
+    size_t logits, ids, wts, sg, qx, g, u, act, qa, down, sg_, su, sact, qs, sout, tok, pair, ntile, te, ts, tn, total;
+    int NS, qx_k, qa_k, qs_k, max_tiles, tile;
+};
+
+Plan plan(const moe_layer_desc* d, int T) {
+    Plan p = {};
+    const int E = d->n_embd, NE = d->n_expert, NU = d->n_used, FE = d->n_ff;
+    const bool sh = d->s_gate != nullptr;
+    p.NS = NU + (sh ? 1 : 0);
+    p.tile = 64;
+    p.max_tiles = gpu_moe_max_tiles(T, NU, NE, p.tile);
+    p.qx_k = r256((long long)T * E);
+    p.qa_k = r256((long long)T * p.NS * FE);
+    p.qs_k = r256((long long)T * FE);
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = o;
+        o += a256(bytes);
+        return at;
+    };
+    p.logits = take((size_t)T * NE * 4);
+    p.ids = take((size_t)T * p.NS * 4);
+    p.wts = take((size_t)T * NU * 4);
+    p.sg = take((size_t)T * 4);
+    p.qx = take(qmatvec_q8_bytes(p.qx_k));
+    p.g = take((size_t)T * p.NS * FE * 4);
+    p.u = take((size_t)T * p.NS * FE * 4);
+    p.act = take((size_t)T * p.NS * FE * 4);
+    p.qa = take(qmatvec_q8_bytes(p.qa_k));
+    p.down = take((size_t)T * p.NS * E * 4);
+    p.sg_ = take(sh ? (size_t)T * FE * 4 : 0);
+    p.su = take(sh ? (size_t)T * FE * 4 : 0);
+    p.sact = take(sh ? (size_t)T * FE * 4 : 0);
+    p.qs = take(sh ? qmatvec_q8_bytes(p.qs_k) : 0);
+    p.sout = take(sh ? (size_t)T * E * 4 : 0);
+    p.tok = take((size_t)T * NU * 4);
+    p.pair = take((size_t)T * NU * 4);
+    p.ntile = take(4);
+    p.te = take((size_t)p.max_tiles * 4);
+    p.ts = take((size_t)p.max_tiles * 4);
+    p.tn = take((size_t)p.max_tiles * 4);
+    p.total = o;
+    return p;
+}
+
+#define CHECK(x)                           \
+    do {                                   \
+        const hipError_t e_ = (x);         \
+        if (e_ != hipSuccess) return e_;   \
+    } while (0)
+
+}  // namespace
+
+extern "C" size_t moe_layer_scratch_bytes(const moe_layer_desc* d, int max_t) {
+    if (!d || max_t <= 0) return 0;
+    return plan(d, max_t).total;
+}
+
+extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x, const float* logits_in, int T,
+                                        float* out, int* ids_out, float* wts_out, void* scratch, size_t scratch_bytes,
+                                        hipStream_t st) {
+    if (!d || !x || !out || T <= 0 || !scratch || ((uintptr_t)scratch & 255)) return hipErrorInvalidValue;
+    const Plan p = plan(d, T);
+    if (scratch_bytes < p.total) return hipErrorInvalidValue;
+    const int E = d->n_embd, NE = d->n_expert, NU = d->n_used, FE = d->n_ff, type = d->type;
+    const bool sh = d->s_gate != nullptr;
+    const size_t rb_in = row_size(type, E), rb_out = row_size(type, FE);
+    char* s = (char*)scratch;
+    float* lg = (float*)(s + p.logits);
+    int* ids = (int*)(s + p.ids);
+    float* wts = (float*)(s + p.wts);
+    float* sg = (float*)(s + p.sg);
+    float* g = (float*)(s + p.g);
+    float* u = (float*)(s + p.u);
+    float* act = (float*)(s + p.act);
+    float* down = (float*)(s + p.down);
+    qmatvec_q8 qx, qa, qs;
+    qmatvec_q8_bind(&qx, s + p.qx, p.qx_k);
+    qmatvec_q8_bind(&qa, s + p.qa, p.qa_k);
+
+    // router logits and routing
+    if (logits_in)
+        lg = (float*)logits_in;
+    else
+        CHECK(qmatvec_launch_batch(0, d->w_router, (size_t)E * 4, x, lg, NE, E, T, st));
+    CHECK(qmatvec_quantize(x, T * E, &qx, st));
+
+    const bool slot = T == 1 && sh;  // moe_core_one: the shared expert as slot NU
+    if (T < 8) {
+        const int ns = slot ? NU + 1 : NU;
+        CHECK(gpu_moe_router(lg, x, d->w_shexp, ids, wts, sg, NE, NU, E, T, st, ns));
+        if (slot)
+            CHECK(qmatvec_launch_q8_id_x(type, d->w_gate, d->w_up, d->s_gate, d->s_up, rb_in, ids, ns, 0, &qx, g, u,
+                                         FE, E, T, st));
+        else
+            CHECK(qmatvec_launch_q8_id_pair(type, d->w_gate, d->w_up, rb_in, ids, ns, 0, &qx, g, u, FE, E, T, st));
+        CHECK(gpu_swiglu(g, u, act, T * ns * FE, &qa, st));
+        if (slot)
+            CHECK(qmatvec_launch_q8_id_x(type, d->w_down, nullptr, d->s_down, nullptr, rb_out, ids, ns, 1, &qa, down,
+                                         nullptr, E, FE, T, st));
+        else
+            CHECK(qmatvec_launch_q8_id(type, d->w_down, rb_out, ids, ns, 1, &qa, down, E, FE, T, st));
+        if (slot) {
+            CHECK(gpu_moe_combine(down, wts, down + (size_t)NU * E, d->w_shexp ? sg : nullptr, out, NU, E, 1, st));
+        } else if (!sh) {
+            CHECK(gpu_moe_combine(down, wts, nullptr, nullptr, out, NU, E, T, st));
+        }
+    } else {
+        CHECK(gpu_moe_router(lg, x, d->w_shexp, ids, wts, sg, NE, NU, E, T, st, NU));
+        int* tok = (int*)(s + p.tok);
+        int* pair = (int*)(s + p.pair);
+        int* ntile = (int*)(s + p.ntile);
+        int* te = (int*)(s + p.te);
+        int* ts = (int*)(s + p.ts);
+        int* tn = (int*)(s + p.tn);
+        CHECK(gpu_moe_group(ids, T, NU, NE, p.tile, tok, pair, ntile, te, ts, tn, st));
+        CHECK(qmatvec_launch_q8_id_batch(type, d->w_gate, rb_in, &qx, g, FE, E, p.max_tiles, p.tile, ntile, te, ts,
+                                         tn, tok, pair, st));
+        CHECK(qmatvec_launch_q8_id_batch(type, d->w_up, rb_in, &qx, u, FE, E, p.max_tiles, p.tile, ntile, te, ts, tn,
+                                         tok, pair, st));
+        CHECK(gpu_swiglu(g, u, act, T * NU * FE, &qa, st));
+        CHECK(qmatvec_launch_q8_id_batch(type, d->w_down, rb_out, &qa, down, E, FE, p.max_tiles, p.tile, ntile, te,
+                                         ts, tn, pair, pair, st));
+        if (!sh) CHECK(gpu_moe_combine(down, wts, nullptr, nullptr, out, NU, E, T, st));
+    }
+    if (sh && !slot) {  // the shared expert as a dense FFN on all T tokens, then the combine
+        float* sgt = (float*)(s + p.sg_);
+        float* sut = (float*)(s + p.su);
+        float* sact = (float*)(s + p.sact);
+        float* sout = (float*)(s + p.sout);
+        qmatvec_q8_bind(&qs, s + p.qs, p.qs_k);
+        CHECK(qmatvec_launch_q8_batch(type, d->s_gate, rb_in, &qx, sgt, FE, FE, E, T, st));
+        CHECK(qmatvec_launch_q8_batch(type, d->s_up, rb_in, &qx, sut, FE, FE, E, T, st));
+        CHECK(gpu_swiglu(sgt, sut, sact, T * FE, &qs, st));
+        CHECK(qmatvec_launch_q8_batch(type, d->s_down, rb_out, &qs, sout, E, E, FE, T, st));
+        CHECK(gpu_moe_combine(down, wts, sout, d->w_shexp ? sg : nullptr, out, NU, E, T, st));
+    }
+    const int ns_used = slot ? NU + 1 : NU;
+    if (ids_out)
+        CHECK(hipMemcpy2DAsync(ids_out, (size_t)NU * 4, ids, (size_t)ns_used * 4, (size_t)NU * 4, T,
+                               hipMemcpyDeviceToDevice, st));
+    if (wts_out) CHECK(hipMemcpyAsync(wts_out, wts, (size_t)T * NU * 4, hipMemcpyDeviceToDevice, st));
+    return hipSuccess;
+}

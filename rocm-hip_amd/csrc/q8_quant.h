@@ -1,0 +1,95 @@
+// q8_quant.h -- the activation quantizer every producer of an expert-matvec input shares (gfx950, wave64).
+//
+// One 256-value block per 256-thread workgroup (four waves), value t of the block in thread t, into both of
+// ggml's activation formats (src/q8_device.h:54-104):
+//   Q8_0 per 32 values: amax, q = round-half-even(x * (127 / amax)) with the unrounded 127 / amax,
+//        d = F16(amax / 127), and the Q8_1 sum s = F16(amax / 127 * sum q) kept as float bits.
+//   Q8_K per 256 values: mx = the signed value of largest |x| (lowest index on ties), iscale = -127 / mx,
+//        q = min(127, round-half-even(iscale * x)), d = 1 / iscale, and the sums of each 16 q.
+// A Q8_0 block is half a wave, so its reductions stay inside the half (xor offsets below 32); the Q8_K
+// arg-max runs over the wave and then over the four waves through LDS.
+#ifndef Q8_QUANT_H
+#define Q8_QUANT_H
+
+#include "moe_common.h"
+
+struct Q8Smem {
+    float a[4];
+    float v[4];
+    int i[4];
+};
+
+__device__ __forceinline__ float fp16_round(float x) { return __half2float(__float2half(x)); }
+
+// Every thread of the 256-thread workgroup calls this the same number of times (it holds barriers);
+// threads past the end of the data pass active = false. blk: the 256-value block index in the output.
+__device__ __forceinline__ void q8_quantize_256(float v, bool active, long long blk, int t, Q8Smem& sh,
+                                                const Q8Out& o) {
+    if (!o.qK) return;  // uniform: no int8 output wanted
+    const int lane = t & 63, w = t >> 6;
+    const long long i = blk * 256 + t;
+    const float a = active ? fabsf(v) : 0.0f;
+
+    float am = a;
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+    const float id = am != 0.0f ? 127.0f / am : 0.0f;
+    const int q0 = active ? (int)rintf(v * id) : 0;
+    int s = q0;
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (active) {
+        o.q0[i] = (int8_t)q0;
+        if ((t & 31) == 0) {
+            const float d = am / 127.0f;
+            o.d0[blk * 8 + (t >> 5)] = fp16_round(d);
+            o.s0[blk * 8 + (t >> 5)] = __float_as_int(fp16_round(d * (float)s));
+        }
+    }
+
+    float ba = a, bv = v;
+    int bi = t;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float oa = __shfl_xor(ba, off, 64), ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (oa > ba || (oa == ba && oi < bi)) {
+            ba = oa;
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) {
+        sh.a[w] = ba;
+        sh.v[w] = bv;
+        sh.i[w] = bi;
+    }
+    __syncthreads();
+    float fa = sh.a[0], fv = sh.v[0];
+    int fi = sh.i[0];
+#pragma unroll
+    for (int k = 1; k < 4; ++k)
+        if (sh.a[k] > fa || (sh.a[k] == fa && sh.i[k] < fi)) {
+            fa = sh.a[k];
+            fv = sh.v[k];
+            fi = sh.i[k];
+        }
+    __syncthreads();  // sh is reused by the next block
+    int q = 0;
+    float iscale = 0.0f;
+    if (fa != 0.0f) {
+        iscale = -127.0f / fv;
+        q = min(127, (int)rintf(iscale * v));
+    }
+    if (!active) q = 0;
+    int s16 = q;
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) s16 += __shfl_xor(s16, off, 64);
+    if (active) {
+        o.qK[i] = (int8_t)q;
+        if (t == 0) o.dK[blk] = fa != 0.0f ? 1.0f / iscale : 0.0f;
+        if ((t & 15) == 0) o.bsK[blk * 16 + (t >> 4)] = s16;
+    }
+}
+
+#endif  // Q8_QUANT_H

@@ -1,0 +1,388 @@
+// vector_ops.hip -- the per-token kernels of the MoE FFN path on gfx950 (wave64) and their C-ABI launchers:
+// activation quantizer, router logits (F32 matvec), router (softmax / top-k / renormalisation), SwiGLU,
+// combine, and the quantizing RMSNorm producer. Semantics: src/gpu_ops.hip and src/matvec_q.hip of the
+// reference; the code is laid out for 64-lane waves.
+
+#include <math.h>
+
+#include "gpu_ops.h"
+#include "host_common.h"
+#include "moe_common.h"
+#include "q8_quant.h"
+#include "qmatvec.h"
+
+static Q8Out q8_out(const qmatvec_q8* q) {
+    Q8Out o = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0};
+    if (q) {
+        o.q0 = q->q0;
+        o.d0 = q->d0;
+        o.qK = q->qK;
+        o.dK = q->dK;
+        o.bsK = q->bsK;
+        o.s0 = q->s0;
+        o.xh = q->xh;
+        o.xh_bf16 = q->xh_bf16;
+    }
+    return o;
+}
+
+__device__ __forceinline__ void half_copy(const Q8Out& o, long long i, float v) {
+    if (!o.xh) return;
+    if (o.xh_bf16) {
+        const uint32_t u = __float_as_uint(v);
+        o.xh[i] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    } else {
+        o.xh[i] = __half_as_ushort(__float2half(v));
+    }
+}
+
+// ------------------------------------------------------------------ quantizer (src/matvec_q.hip:1245-1250)
+
+__global__ void __launch_bounds__(256) k_quantize_q8(const float* x, int n, Q8Out o) {
+    __shared__ Q8Smem sh;
+    const int t = threadIdx.x;
+    const long long i = (long long)blockIdx.x * 256 + t;
+    const bool act = i < n;
+    const float v = act ? x[i] : 0.0f;
+    if (act) half_copy(o, i, v);
+    q8_quantize_256(v, act, blockIdx.x, t, sh, o);
+}
+
+// ------------------------------------------------------------------ SwiGLU (src/gpu_ops.hip:103-114)
+
+__global__ void __launch_bounds__(256) k_swiglu(const float* g, const float* u, float* out, int n, Q8Out o) {
+    __shared__ Q8Smem sh;
+    const int t = threadIdx.x;
+    const long long i = (long long)blockIdx.x * 256 + t;
+    float v = 0.0f;
+    if (i < n) {
+        const float a = g[i];
+        v = a / (1.0f + __expf(-a)) * u[i];
+        out[i] = v;
+        half_copy(o, i, v);
+    }
+    q8_quantize_256(v, i < n, blockIdx.x, t, sh, o);
+}
+
+// ------------------------------------------------------------------ combine (src/gpu_ops.hip:245-264)
+
+// out = w0 d0 + w1 d1 + ... in slot order (each expert's output first times exp_scale[id] when set), then the
+// shared expert (times sg when set)
+__global__ void __launch_bounds__(256) k_combine(const float* down, const float* wts, const float* shared,
+                                                 const float* sg, const int* ids, const float* exp_scale, float* out,
+                                                 int nu, int n) {
+    const int t = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float* d = down + (size_t)t * nu * n + i;
+    const float* w = wts ? wts + (size_t)t * nu : nullptr;
+    float acc;
+    if (!wts) {  // weight 1 per expert
+        acc = d[0];
+        for (int j = 1; j < nu; ++j) acc += d[(size_t)j * n];
+    } else if (exp_scale) {
+        const int* e = ids + (size_t)t * nu;
+        acc = (d[0] * exp_scale[e[0]]) * w[0];
+        for (int j = 1; j < nu; ++j) acc += (d[(size_t)j * n] * exp_scale[e[j]]) * w[j];
+    } else {
+        acc = w[0] * d[0];
+        for (int j = 1; j < nu; ++j) acc += w[j] * d[(size_t)j * n];
+    }
+    if (shared) acc += sg ? shared[(size_t)t * n + i] * sg[t] : shared[(size_t)t * n + i];
+    out[(size_t)t * n + i] = acc;
+}
+
+// ------------------------------------------------------------------ RMSNorm producer (src/gpu_ops.hip:24-56)
+
+// One row per workgroup: x_out = x_in + add; y = x_out / sqrt(mean(x_out^2) + eps) * w, quantized per 256
+__global__ void __launch_bounds__(256) k_add_rmsnorm(const float* x_in, const float* add, float* x_out,
+                                                     const float* w, float* y, int n, float eps, Q8Out o) {
+    __shared__ Q8Smem sh;
+    __shared__ float part[4];
+    const int t = threadIdx.x, row = blockIdx.x;
+    const float* xr = x_in + (size_t)row * n;
+    const float* ar = add ? add + (size_t)row * n : nullptr;
+    float ss = 0.0f;
+    for (int i = t; i < n; i += 256) {
+        const float v = ar ? xr[i] + ar[i] : xr[i];
+        ss += v * v;
+    }
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) part[t >> 6] = ss;
+    __syncthreads();
+    const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float inv = 1.0f / sqrtf(tot / (float)n + eps);
+    const int nb = (n + 255) / 256;
+    for (int b = 0; b < nb; ++b) {
+        const int i = b * 256 + t;
+        const bool act = i < n;
+        float v = 0.0f;
+        if (act) {
+            const float xv = ar ? xr[i] + ar[i] : xr[i];
+            if (ar) x_out[(size_t)row * n + i] = xv;
+            v = xv * inv * (w ? w[i] : 1.0f);
+            y[(size_t)row * n + i] = v;
+            half_copy(o, (long long)row * n + i, v);
+        }
+        q8_quantize_256(v, act, (long long)row * nb + b, t, sh, o);
+    }
+}
+
+// ------------------------------------------------------------------ router logits: F32 matvec
+
+// Decode: one wave per row, 16-byte loads, x re-read from L1 / L2. y[row] = W[row] . x
+__global__ void __launch_bounds__(64) k_matvec_f32(const float* W, long long ldw, const float* x, float* y, int N,
+                                                  int K) {
+    const int row = blockIdx.x, lane = threadIdx.x;
+    if (row >= N) return;
+    const float* wr = W + (size_t)row * ldw;
+    float acc = 0.0f;
+    if ((K & 3) == 0 && (((uintptr_t)wr | (uintptr_t)x) & 15) == 0) {
+        const float4* w4 = (const float4*)wr;
+        const float4* x4 = (const float4*)x;
+        for (int i = lane; i < K / 4; i += 64) {
+            const float4 a = w4[i], b = x4[i];
+            acc = fmaf(a.x, b.x, acc);
+            acc = fmaf(a.y, b.y, acc);
+            acc = fmaf(a.z, b.z, acc);
+            acc = fmaf(a.w, b.w, acc);
+        }
+    } else {
+        for (int i = lane; i < K; i += 64) acc = fmaf(wr[i], x[i], acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) y[row] = acc;
+}
+
+// Prefill: tiles of 64 tokens x 64 rows, K staged through LDS in chunks of 32; each thread 4 x 4 outputs.
+#define MF_TT 64
+#define MF_TR 64
+#define MF_KC 32
+__global__ void __launch_bounds__(256) k_matmul_f32(const float* W, long long ldw, const float* X, float* Y, int N,
+                                                   int K, int T) {
+    __shared__ float sw[MF_KC][MF_TR + 4];
+    __shared__ float sx[MF_KC][MF_TT + 4];
+    const int tid = threadIdx.x;
+    const int r0 = blockIdx.x * MF_TR, t0 = blockIdx.y * MF_TT;
+    const int tr = (tid & 15) * 4, tt = (tid >> 4) * 4;
+    float acc[4][4] = {};
+    for (int k0 = 0; k0 < K; k0 += MF_KC) {
+        for (int i = tid; i < MF_TR * MF_KC; i += 256) {
+            const int r = i / MF_KC, k = i % MF_KC;
+            sw[k][r] = (r0 + r < N && k0 + k < K) ? W[(size_t)(r0 + r) * ldw + k0 + k] : 0.0f;
+            sx[k][r] = (t0 + r < T && k0 + k < K) ? X[(size_t)(t0 + r) * K + k0 + k] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (int k = 0; k < MF_KC; ++k) {
+            float a[4], b[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                a[j] = sx[k][tt + j];
+                b[j] = sw[k][tr + j];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (t0 + tt + i < T && r0 + tr + j < N) Y[(size_t)(t0 + tt + i) * N + r0 + tr + j] = acc[i][j];
+}
+
+// ------------------------------------------------------------------ router (src/gpu_ops.hip:185-241)
+
+// One wave per token. Lane l holds the logits of experts l + 64 j (j < PL) in registers. The selection runs
+// n_used rounds of a wave arg-max on the logits (softmax is strictly monotonic, so this is the order of the
+// probabilities), ties to the lower expert index; the selected probabilities exp(l - max) / sum are then
+// renormalised by max(sum of them, 6.103515625e-5).
+template <int PL>
+__global__ void __launch_bounds__(64) k_router(const float* logits, const float* x, const float* w_shexp, int* ids,
+                                               float* wts, float* sg, int ne, int nu, int n, int ids_stride) {
+    __shared__ float sel_p[64];
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const float* lg = logits + (size_t)t * ne;
+
+    if (w_shexp) {  // the shared-expert gate (uniform branch)
+        const float* xr = x + (size_t)t * n;
+        float d = 0.0f;
+        if ((n & 3) == 0 && (((uintptr_t)xr | (uintptr_t)w_shexp) & 15) == 0) {
+            for (int i = lane; i < n / 4; i += 64) {
+                const float4 a = ((const float4*)xr)[i], b = ((const float4*)w_shexp)[i];
+                d += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+            }
+        } else {
+            for (int i = lane; i < n; i += 64) d += xr[i] * w_shexp[i];
+        }
+        d = wave_sum(d);
+        if (lane == 0) sg[t] = 1.0f / (1.0f + expf(-d));
+    }
+
+    float v[PL];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PL; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = e < ne ? lg[e] : -INFINITY;
+        mx = fmaxf(mx, v[j]);
+    }
+    mx = wave_max(mx);
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PL; ++j)
+        if (lane + 64 * j < ne) sum += expf(v[j] - mx);
+    sum = wave_sum(sum);
+    const float inv = 1.0f / sum;
+
+    int* id_row = ids + (size_t)t * ids_stride;
+    for (int r = 0; r < nu; ++r) {
+        float bv = v[0];
+        int bj = 0;
+#pragma unroll
+        for (int j = 1; j < PL; ++j)
+            if (v[j] > bv) {
+                bv = v[j];
+                bj = j;
+            }
+        int be = lane + 64 * bj;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, 64);
+            const int oe = __shfl_xor(be, off, 64);
+            if (ov > bv || (ov == bv && oe < be)) {
+                bv = ov;
+                be = oe;
+            }
+        }
+        if (lane == 0) {
+            id_row[r] = be;
+            sel_p[r] = expf(bv - mx) * inv;
+        }
+        if ((be & 63) == lane) {
+#pragma unroll
+            for (int j = 0; j < PL; ++j)
+                if (j == (be >> 6)) v[j] = -INFINITY;
+        }
+    }
+    if (lane == 0 && ids_stride > nu) id_row[nu] = -1;
+    __syncthreads();
+    if (lane == 0) {
+        float ws = 0.0f;
+        for (int r = 0; r < nu; ++r) ws += sel_p[r];
+        ws = fmaxf(ws, 6.103515625e-5f);
+        for (int r = 0; r < nu; ++r) wts[(size_t)t * nu + r] = sel_p[r] / ws;
+    }
+}
+
+// ------------------------------------------------------------------ C ABI
+
+extern "C" size_t qmatvec_q8_bytes(int max_k) {
+    const size_t k = (size_t)max_k;
+    auto a16 = [](size_t v) { return (v + 15) & ~(size_t)15; };
+    return 2 * a16(k) + 2 * a16(k / 32 * 4) + a16(k / 256 * 4) + a16(k / 16 * 4);
+}
+
+extern "C" void qmatvec_q8_bind(qmatvec_q8* q, void* mem, int max_k) {
+    const size_t k = (size_t)max_k;
+    auto a16 = [](size_t v) { return (v + 15) & ~(size_t)15; };
+    char* p = (char*)mem;
+    q->q0 = (int8_t*)p;
+    p += a16(k);
+    q->qK = (int8_t*)p;
+    p += a16(k);
+    q->d0 = (float*)p;
+    p += a16(k / 32 * 4);
+    q->dK = (float*)p;
+    p += a16(k / 256 * 4);
+    q->bsK = (int32_t*)p;
+    p += a16(k / 16 * 4);
+    q->s0 = (int32_t*)p;
+    q->max_k = max_k;
+    q->xh = nullptr;
+    q->xh_bf16 = 0;
+}
+
+extern "C" hipError_t qmatvec_quantize(const float* x, int K, const qmatvec_q8* q, hipStream_t stream) {
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (!q || K <= 0 || K % 32 != 0 || K > q->max_k) return hipErrorInvalidValue;
+    return launch_kernel(k_quantize_q8, dim3((K + 255) / 256), dim3(256), 0, stream, x, K, q8_out(q));
+}
+
+extern "C" int qmatvec_supported(int type) { return type == QT_F32; }
+
+extern "C" hipError_t qmatvec_launch(int type, const void* W, size_t row_bytes, const float* x, float* y, int N, int K,
+                                     hipStream_t stream) {
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (type != QT_F32) return hipErrorInvalidDeviceFunction;
+    if (N <= 0 || K <= 0 || row_bytes != (size_t)K * 4) return hipErrorInvalidValue;
+    return launch_kernel(k_matvec_f32, dim3(N), dim3(64), 0, stream, (const float*)W, (long long)K, x, y, N, K);
+}
+
+extern "C" hipError_t qmatvec_launch_batch(int type, const void* W, size_t row_bytes, const float* x, float* y, int N,
+                                           int K, int T, hipStream_t stream) {
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (type != QT_F32) return hipErrorInvalidDeviceFunction;
+    if (N <= 0 || K <= 0 || T <= 0 || row_bytes != (size_t)K * 4) return hipErrorInvalidValue;
+    if (T == 1) return qmatvec_launch(type, W, row_bytes, x, y, N, K, stream);
+    return launch_kernel(k_matmul_f32, dim3((N + MF_TR - 1) / MF_TR, (T + MF_TT - 1) / MF_TT), dim3(256), 0, stream,
+                         (const float*)W, (long long)K, x, y, N, K, T);
+}
+
+extern "C" hipError_t gpu_add_rmsnorm(const float* x_in, const float* add, float* x_out, const float* w, float* y,
+                                      int n, int T, float eps, const qmatvec_q8* q8, hipStream_t stream) {
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (T <= 0 || n <= 0 || (q8 && (n % 256 != 0 || (long long)n * T > q8->max_k)) || (add && x_out == x_in))
+        return hipErrorInvalidValue;
+    return launch_kernel(k_add_rmsnorm, dim3(T), dim3(256), 0, stream, x_in, add, x_out, w, y, n, eps, q8_out(q8));
+}
+
+extern "C" hipError_t gpu_swiglu(const float* g, const float* u, float* out, int n, const qmatvec_q8* q8,
+                                 hipStream_t stream) {
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (n <= 0 || (q8 && (n % 32 != 0 || n > q8->max_k))) return hipErrorInvalidValue;
+    return launch_kernel(k_swiglu, dim3((n + 255) / 256), dim3(256), 0, stream, g, u, out, n, q8_out(q8));
+}
+
+extern "C" hipError_t gpu_moe_router(const float* logits, const float* x, const float* w_shexp, int* ids, float* wts,
+                                     float* sg, int n_expert, int n_used, int n, int T, hipStream_t stream,
+                                     int ids_stride) {
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (n_expert <= 0 || n_expert > 1024 || n_used <= 0 || n_used > 64 || n_used > n_expert || T <= 0)
+        return hipErrorInvalidValue;
+    if (ids_stride == 0) ids_stride = n_used;
+    if (ids_stride < n_used || (w_shexp && (!x || !sg || n <= 0))) return hipErrorInvalidValue;
+    const dim3 g(T), b(64);
+    if (n_expert <= 64)
+        return launch_kernel(k_router<1>, g, b, 0, stream, logits, x, w_shexp, ids, wts, sg, n_expert, n_used, n,
+                             ids_stride);
+    if (n_expert <= 128)
+        return launch_kernel(k_router<2>, g, b, 0, stream, logits, x, w_shexp, ids, wts, sg, n_expert, n_used, n,
+                             ids_stride);
+    if (n_expert <= 256)
+        return launch_kernel(k_router<4>, g, b, 0, stream, logits, x, w_shexp, ids, wts, sg, n_expert, n_used, n,
+                             ids_stride);
+    if (n_expert <= 512)
+        return launch_kernel(k_router<8>, g, b, 0, stream, logits, x, w_shexp, ids, wts, sg, n_expert, n_used, n,
+                             ids_stride);
+    return launch_kernel(k_router<16>, g, b, 0, stream, logits, x, w_shexp, ids, wts, sg, n_expert, n_used, n,
+                         ids_stride);
+}
+
+extern "C" hipError_t gpu_moe_combine_scaled(const float* down, const float* wts, const float* shared, const float* sg,
+                                             const int* ids, const float* exp_scale, float* out, int n_used, int n,
+                                             int T, hipStream_t stream) {
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (n_used <= 0 || n <= 0 || T <= 0 || (exp_scale && (!ids || !wts))) return hipErrorInvalidValue;
+    return launch_kernel(k_combine, dim3((n + 255) / 256, T), dim3(256), 0, stream, down, wts, shared, sg, ids,
+                         exp_scale, out, n_used, n);
+}
+
+extern "C" hipError_t gpu_moe_combine(const float* down, const float* wts, const float* shared, const float* sg,
+                                      float* out, int n_used, int n, int T, hipStream_t stream) {
+    return gpu_moe_combine_scaled(down, wts, shared, sg, nullptr, nullptr, out, n_used, n, T, stream);
+}
