@@ -5,20 +5,31 @@ import sys
 import numpy as np
 
 
+# Device tensors handed to asynchronous launches stay referenced until the next host() synchronises, so the
+# caching allocator cannot hand their memory to a later allocation while a kernel may still read it.
+_live = []
+
+
 def dev(a):
     import torch
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    _live.append(t)
+    return t
 
 
 def zeros(shape, dtype):
     import torch
-    return torch.zeros(shape, dtype=dtype, device="cuda")
+    t = torch.zeros(shape, dtype=dtype, device="cuda")
+    _live.append(t)
+    return t
 
 
 def host(t):
     import torch
     torch.cuda.synchronize()
-    return t.cpu().numpy()
+    out = t.cpu().numpy()
+    _live.clear()
+    return out
 
 
 def rel_l2(got, want):
