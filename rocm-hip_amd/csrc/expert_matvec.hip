@@ -40,8 +40,10 @@ __device__ __forceinline__ void load_unit(const uint8_t* vrow, const uint8_t* sr
         load_native<TYPE>(vrow, u, w);
 }
 
-// R rows (row0 + r * stride) of the matrix at (vbase, sbase) against one input row; returns the group sums
-template <int TYPE, bool PACKED, int L, int R>
+// R rows (row0 + r * stride) of the matrix at (vbase, sbase) against one input row; returns the group sums.
+// NUPL > 0: every lane has exactly NUPL units (nu == NUPL * L) and all R * NUPL weight loads (and the NUPL
+// activation loads) are issued before any arithmetic; NUPL == 0: a loop over the lane's units.
+template <int TYPE, bool PACKED, int L, int R, int NUPL>
 __device__ __forceinline__ void rows_dot(const uint8_t* vbase, const uint8_t* sbase, long long vrb, long long srb,
                                          int row0, int stride, int nrows, const int8_t* xq, const float* xd,
                                          const int* xbs, int K, int gl, float acc[R]) {
@@ -55,14 +57,29 @@ __device__ __forceinline__ void rows_dot(const uint8_t* vbase, const uint8_t* sb
         sr[r] = PACKED ? sbase + (long long)row * srb : nullptr;
         acc[r] = 0.0f;
     }
-    for (int u = gl; u < nu; u += L) {
-        XUnit<TYPE> x;
-        load_x<TYPE>(xq, xd, xbs, u, x);
-        WUnit<TYPE> w[R];
+    if constexpr (NUPL > 0) {
+        WUnit<TYPE> w[NUPL][R];
+        XUnit<TYPE> x[NUPL];
 #pragma unroll
-        for (int r = 0; r < R; ++r) load_unit<TYPE, PACKED>(vr[r], sr[r], u, nu, w[r]);
+        for (int i = 0; i < NUPL; ++i)
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] += term<TYPE>(w[r], x, u);
+            for (int r = 0; r < R; ++r) load_unit<TYPE, PACKED>(vr[r], sr[r], gl + i * L, nu, w[i][r]);
+#pragma unroll
+        for (int i = 0; i < NUPL; ++i) load_x<TYPE>(xq, xd, xbs, gl + i * L, x[i]);
+#pragma unroll
+        for (int i = 0; i < NUPL; ++i)
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] += term<TYPE>(w[i][r], x[i], gl + i * L);
+    } else {
+        for (int u = gl; u < nu; u += L) {
+            XUnit<TYPE> x;
+            load_x<TYPE>(xq, xd, xbs, u, x);
+            WUnit<TYPE> w[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) load_unit<TYPE, PACKED>(vr[r], sr[r], u, nu, w[r]);
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] += term<TYPE>(w[r], x, u);
+        }
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<L>(acc[r]);
@@ -77,7 +94,7 @@ __device__ __forceinline__ void act_row(const MvArgs& a, long long in_row, const
 }
 
 // grid (row blocks, n_used * (1 or 2) slots, T tokens) in id mode; (row blocks, 1 or 2 matrices, T) dense
-template <int TYPE, bool PACKED, int L, int R>
+template <int TYPE, bool PACKED, int L, int R, int NUPL>
 __global__ void __launch_bounds__(256) k_expert_mv(MvArgs a) {
     constexpr int G = 64 / L;  // row groups per wave
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -109,7 +126,7 @@ __global__ void __launch_bounds__(256) k_expert_mv(MvArgs a) {
     const int* xbs;
     act_row<TYPE>(a, in_row, xq, xd, xbs);
     float acc[R];
-    rows_dot<TYPE, PACKED, L, R>(vbase, sbase, a.vrb, a.srb, row0, G, nrows, xq, xd, xbs, a.K, gl, acc);
+    rows_dot<TYPE, PACKED, L, R, NUPL>(vbase, sbase, a.vrb, a.srb, row0, G, nrows, xq, xd, xbs, a.K, gl, acc);
     if (gl == 0) {
         float* y = (mi & 1 ? a.y2 : a.y) + out_row * a.ldy;
 #pragma unroll
@@ -141,7 +158,7 @@ __global__ void __launch_bounds__(256) k_expert_entries(MvArgs a, const int* n_t
         const int* xbs;
         act_row<TYPE>(a, in_rows[st + i], xq, xd, xbs);
         float acc[R];
-        rows_dot<TYPE, PACKED, L, R>(vbase, sbase, a.vrb, a.srb, row0, G, a.N, xq, xd, xbs, a.K, gl, acc);
+        rows_dot<TYPE, PACKED, L, R, 0>(vbase, sbase, a.vrb, a.srb, row0, G, a.N, xq, xd, xbs, a.K, gl, acc);
         if (gl == 0) {
             float* y = a.y + (long long)out_rows[st + i] * a.N;
 #pragma unroll
@@ -232,24 +249,54 @@ bool find_packed(const void* W, int type, int K, size_t row_bytes, const uint8_t
     return true;
 }
 
-int lanes_for(int type, int K) {
+// Lanes per row L and units per lane NUPL: the largest L in {64, 32, 16, 8} that splits the row's units evenly
+// into at most 4 per lane (then every load is issued up front); else the largest L not above the unit count,
+// with a loop over units (NUPL 0)
+struct MvShape {
+    int L, nupl;
+};
+MvShape mv_shape(int type, int K) {
     const int nu = fmt_units(type, K);
+    for (int L = 64; L >= 8; L /= 2)
+        if (nu % L == 0 && nu / L <= 4) return {L, nu / L};
     int L = 64;
-    while (L > 8 && (L > nu || nu % L != 0)) L /= 2;
-    return L;
+    while (L > 8 && L > nu) L /= 2;
+    return {L, 0};
+}
+int lanes_for(int type, int K) { return mv_shape(type, K).L; }
+
+// Rows in flight per lane group: about four loads of weights per lane
+constexpr int rows_in_flight(int L, int nupl) { return nupl >= 4 ? 1 : nupl >= 2 ? 2 : nupl == 1 ? 4 : (L == 64 ? 4 : 2); }
+int rows_per_block(int L, int nupl) { return 4 * rows_in_flight(L, nupl) * (64 / L); }
+
+template <int TYPE, bool PACKED, int L, int NUPL>
+hipError_t launch_mv_l(const MvArgs& a, dim3 yz, int nrows, hipStream_t st) {
+    constexpr int R = rows_in_flight(L, NUPL);
+    const int rpb = 4 * R * (64 / L);
+    const dim3 g((nrows + rpb - 1) / rpb, yz.y, yz.z), b(256);
+    return launch_kernel(k_expert_mv<TYPE, PACKED, L, R, NUPL>, g, b, 0, st, a);
 }
 
-constexpr int rows_in_flight(int L) { return L == 64 ? 4 : 2; }
-int rows_per_block(int L) { return 4 * rows_in_flight(L) * (64 / L); }
+template <int TYPE, bool PACKED, int L>
+hipError_t launch_mv_n(const MvArgs& a, dim3 yz, int nupl, int nrows, hipStream_t st) {
+    if constexpr (PACKED) {
+        switch (nupl) {
+        case 1: return launch_mv_l<TYPE, PACKED, L, 1>(a, yz, nrows, st);
+        case 2: return launch_mv_l<TYPE, PACKED, L, 2>(a, yz, nrows, st);
+        case 3: return launch_mv_l<TYPE, PACKED, L, 3>(a, yz, nrows, st);
+        case 4: return launch_mv_l<TYPE, PACKED, L, 4>(a, yz, nrows, st);
+        }
+    }
+    return launch_mv_l<TYPE, PACKED, L, 0>(a, yz, nrows, st);
+}
 
 template <int TYPE, bool PACKED>
-hipError_t launch_mv_t(const MvArgs& a, dim3 grid_yz, int L, int nrows, hipStream_t st) {
-    const dim3 g((nrows + rows_per_block(L) - 1) / rows_per_block(L), grid_yz.y, grid_yz.z), b(256);
-    switch (L) {
-    case 64: return launch_kernel(k_expert_mv<TYPE, PACKED, 64, rows_in_flight(64)>, g, b, 0, st, a);
-    case 32: return launch_kernel(k_expert_mv<TYPE, PACKED, 32, rows_in_flight(32)>, g, b, 0, st, a);
-    case 16: return launch_kernel(k_expert_mv<TYPE, PACKED, 16, rows_in_flight(16)>, g, b, 0, st, a);
-    default: return launch_kernel(k_expert_mv<TYPE, PACKED, 8, rows_in_flight(8)>, g, b, 0, st, a);
+hipError_t launch_mv_t(const MvArgs& a, dim3 yz, MvShape sh, int nrows, hipStream_t st) {
+    switch (sh.L) {
+    case 64: return launch_mv_n<TYPE, PACKED, 64>(a, yz, sh.nupl, nrows, st);
+    case 32: return launch_mv_n<TYPE, PACKED, 32>(a, yz, sh.nupl, nrows, st);
+    case 16: return launch_mv_n<TYPE, PACKED, 16>(a, yz, sh.nupl, nrows, st);
+    default: return launch_mv_n<TYPE, PACKED, 8>(a, yz, sh.nupl, nrows, st);
     }
 }
 
@@ -257,9 +304,9 @@ template <int TYPE, bool PACKED>
 hipError_t launch_entries_t(const MvArgs& a, int max_tiles, int L, const int32_t* n_tiles, const int32_t* tile_e,
                             const int32_t* tile_start, const int32_t* tile_n, const int32_t* in_rows,
                             const int32_t* out_rows, hipStream_t st) {
-    const dim3 g((a.N + rows_per_block(L) - 1) / rows_per_block(L), max_tiles), b(256);
-#define ENTRIES_CASE(LL)                                                                                          \
-    return launch_kernel(k_expert_entries<TYPE, PACKED, LL, rows_in_flight(LL)>, g, b, 0, st, a, n_tiles, tile_e, \
+    const dim3 g((a.N + rows_per_block(L, 0) - 1) / rows_per_block(L, 0), max_tiles), b(256);
+#define ENTRIES_CASE(LL)                                                                                             \
+    return launch_kernel(k_expert_entries<TYPE, PACKED, LL, rows_in_flight(LL, 0)>, g, b, 0, st, a, n_tiles, tile_e, \
                          tile_start, tile_n, in_rows, out_rows)
     switch (L) {
     case 64: ENTRIES_CASE(64);
@@ -270,12 +317,13 @@ hipError_t launch_entries_t(const MvArgs& a, int max_tiles, int L, const int32_t
 #undef ENTRIES_CASE
 }
 
-hipError_t launch_mv(int type, bool packed, const MvArgs& a, dim3 yz, int L, int nrows, hipStream_t st) {
+hipError_t launch_mv(int type, bool packed, const MvArgs& a, dim3 yz, int nrows, hipStream_t st) {
+    const MvShape sh = mv_shape(type, a.K);
     switch (type) {
-    case QT_Q8_0: return packed ? launch_mv_t<QT_Q8_0, true>(a, yz, L, nrows, st) : launch_mv_t<QT_Q8_0, false>(a, yz, L, nrows, st);
-    case QT_ROCMFP4: return packed ? launch_mv_t<QT_ROCMFP4, true>(a, yz, L, nrows, st) : launch_mv_t<QT_ROCMFP4, false>(a, yz, L, nrows, st);
-    case QT_ROCMFP4_FAST: return packed ? launch_mv_t<QT_ROCMFP4_FAST, true>(a, yz, L, nrows, st) : launch_mv_t<QT_ROCMFP4_FAST, false>(a, yz, L, nrows, st);
-    case QT_Q4_K: return packed ? launch_mv_t<QT_Q4_K, true>(a, yz, L, nrows, st) : launch_mv_t<QT_Q4_K, false>(a, yz, L, nrows, st);
+    case QT_Q8_0: return packed ? launch_mv_t<QT_Q8_0, true>(a, yz, sh, nrows, st) : launch_mv_t<QT_Q8_0, false>(a, yz, sh, nrows, st);
+    case QT_ROCMFP4: return packed ? launch_mv_t<QT_ROCMFP4, true>(a, yz, sh, nrows, st) : launch_mv_t<QT_ROCMFP4, false>(a, yz, sh, nrows, st);
+    case QT_ROCMFP4_FAST: return packed ? launch_mv_t<QT_ROCMFP4_FAST, true>(a, yz, sh, nrows, st) : launch_mv_t<QT_ROCMFP4_FAST, false>(a, yz, sh, nrows, st);
+    case QT_Q4_K: return packed ? launch_mv_t<QT_Q4_K, true>(a, yz, sh, nrows, st) : launch_mv_t<QT_Q4_K, false>(a, yz, sh, nrows, st);
     }
     return hipErrorInvalidDeviceFunction;
 }
@@ -419,8 +467,7 @@ extern "C" hipError_t qmatvec_launch_q8_id_x(int type, const void* W, const void
     a.ldy = N;
     a.N = a.N2 = N;
     a.K = K;
-    const int L = lanes_for(type, K);
-    return launch_mv(type, packed, a, dim3(1, n_used * (W2 ? 2 : 1), T), L, N, stream);
+    return launch_mv(type, packed, a, dim3(1, n_used * (W2 ? 2 : 1), T), N, stream);
 }
 
 extern "C" hipError_t qmatvec_launch_q8_id(int type, const void* W, size_t row_bytes, const int32_t* ids, int n_used,
@@ -456,7 +503,7 @@ static hipError_t dense(int type, const void* W, int N, float* y, const void* W2
     a.N = N;
     a.N2 = W2 ? N2 : 0;
     a.K = K;
-    return launch_mv(type, packed, a, dim3(1, W2 ? 2 : 1, T), lanes_for(type, K), W2 && N2 > N ? N2 : N, stream);
+    return launch_mv(type, packed, a, dim3(1, W2 ? 2 : 1, T), W2 && N2 > N ? N2 : N, stream);
 }
 
 extern "C" hipError_t qmatvec_launch_q8_pair(int type, const void* W, int N, float* y, const void* W2, int N2,

@@ -70,19 +70,74 @@ __device__ __forceinline__ void q4k_scale_min(int j, const uint32_t s[3], int& s
     }
 }
 
-// Sum over groups of G consecutive lanes of the wave (G a power of two <= 64)
+// Cross-lane moves inside a row of 16 lanes (DPP): quad_perm [1,0,3,2] (0xB1), quad_perm [2,3,0,1] (0x4E),
+// row_half_mirror (0x141), row_mirror (0x140). After the xor-1 and xor-2 steps every lane of a quad holds the
+// quad's value, so the two mirrors combine halves and rows: group sums of 2, 4, 8 and 16 lanes, in every lane.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+}
+// Lane l <- lane l ^ 16 within each half-wave (ds_swizzle, bit mode: and 0x1f, xor 0x10)
+__device__ __forceinline__ float swz_xor16(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));
+}
+
+// Sum over groups of G consecutive lanes (G a power of two <= 64); every lane of a group gets the group's sum
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if constexpr (G >= 2) v += dpp_f<0xb1>(v);
+    if constexpr (G >= 4) v += dpp_f<0x4e>(v);
+    if constexpr (G >= 8) v += dpp_f<0x141>(v);
+    if constexpr (G >= 16) v += dpp_f<0x140>(v);
+    if constexpr (G >= 32) v += swz_xor16(v);
+    if constexpr (G >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (G >= 2) v = fmaxf(v, dpp_f<0xb1>(v));
+    if constexpr (G >= 4) v = fmaxf(v, dpp_f<0x4e>(v));
+    if constexpr (G >= 8) v = fmaxf(v, dpp_f<0x141>(v));
+    if constexpr (G >= 16) v = fmaxf(v, dpp_f<0x140>(v));
+    if constexpr (G >= 32) v = fmaxf(v, swz_xor16(v));
+    if constexpr (G >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
+// The value a reduction step of width S (1, 2, 4, 8, 16, 32) pairs this lane with: after the steps below S,
+// every lane of an S-lane group holds that group's value, so combining with the partner widens it to 2S.
+template <int S>
+__device__ __forceinline__ int partner_i(int v) {
+    if constexpr (S == 1) return dpp_i<0xb1>(v);
+    if constexpr (S == 2) return dpp_i<0x4e>(v);
+    if constexpr (S == 4) return dpp_i<0x141>(v);
+    if constexpr (S == 8) return dpp_i<0x140>(v);
+    if constexpr (S == 16) return __builtin_amdgcn_ds_swizzle(v, 0x401f);
+    if constexpr (S == 32) return __shfl_xor(v, 32, 64);
+    return v;
+}
+template <int S>
+__device__ __forceinline__ float partner_f(float v) {
+    return __int_as_float(partner_i<S>(__float_as_int(v)));
+}
+
+template <int G>
+__device__ __forceinline__ int group_sum_i(int v) {
+    if constexpr (G >= 2) v += partner_i<1>(v);
+    if constexpr (G >= 4) v += partner_i<2>(v);
+    if constexpr (G >= 8) v += partner_i<4>(v);
+    if constexpr (G >= 16) v += partner_i<8>(v);
+    if constexpr (G >= 32) v += partner_i<16>(v);
+    if constexpr (G >= 64) v += partner_i<32>(v);
     return v;
 }
 
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
+__device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 
 #endif  // MOE_COMMON_H

@@ -21,6 +21,19 @@ struct Q8Smem {
 
 __device__ __forceinline__ float fp16_round(float x) { return __half2float(__float2half(x)); }
 
+// One step of the Q8_K arg-max: the larger |x|, the lower index on ties (a total order, so the result does not
+// depend on the pairing pattern)
+template <int S>
+__device__ __forceinline__ void argmax_step(float& ba, float& bv, int& bi) {
+    const float oa = partner_f<S>(ba), ov = partner_f<S>(bv);
+    const int oi = partner_i<S>(bi);
+    if (oa > ba || (oa == ba && oi < bi)) {
+        ba = oa;
+        bv = ov;
+        bi = oi;
+    }
+}
+
 // Every thread of the 256-thread workgroup calls this the same number of times (it holds barriers);
 // threads past the end of the data pass active = false. blk: the 256-value block index in the output.
 __device__ __forceinline__ void q8_quantize_256(float v, bool active, long long blk, int t, Q8Smem& sh,
@@ -30,14 +43,10 @@ __device__ __forceinline__ void q8_quantize_256(float v, bool active, long long 
     const long long i = blk * 256 + t;
     const float a = active ? fabsf(v) : 0.0f;
 
-    float am = a;
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+    const float am = group_max<32>(a);
     const float id = am != 0.0f ? 127.0f / am : 0.0f;
     const int q0 = active ? (int)rintf(v * id) : 0;
-    int s = q0;
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    const int s = group_sum_i<32>(q0);
     if (active) {
         o.q0[i] = (int8_t)q0;
         if ((t & 31) == 0) {
@@ -49,16 +58,12 @@ __device__ __forceinline__ void q8_quantize_256(float v, bool active, long long 
 
     float ba = a, bv = v;
     int bi = t;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float oa = __shfl_xor(ba, off, 64), ov = __shfl_xor(bv, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
-        if (oa > ba || (oa == ba && oi < bi)) {
-            ba = oa;
-            bv = ov;
-            bi = oi;
-        }
-    }
+    argmax_step<1>(ba, bv, bi);
+    argmax_step<2>(ba, bv, bi);
+    argmax_step<4>(ba, bv, bi);
+    argmax_step<8>(ba, bv, bi);
+    argmax_step<16>(ba, bv, bi);
+    argmax_step<32>(ba, bv, bi);
     if (lane == 0) {
         sh.a[w] = ba;
         sh.v[w] = bv;
@@ -82,9 +87,7 @@ __device__ __forceinline__ void q8_quantize_256(float v, bool active, long long 
         q = min(127, (int)rintf(iscale * v));
     }
     if (!active) q = 0;
-    int s16 = q;
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) s16 += __shfl_xor(s16, off, 64);
+    const int s16 = group_sum_i<16>(q);
     if (active) {
         o.qK[i] = (int8_t)q;
         if (t == 0) o.dK[blk] = fa != 0.0f ? 1.0f / iscale : 0.0f;

@@ -130,17 +130,28 @@ __global__ void __launch_bounds__(256) k_add_rmsnorm(const float* x_in, const fl
 
 // ------------------------------------------------------------------ router logits: F32 matvec
 
-// Decode: one wave per row, 16-byte loads, x re-read from L1 / L2. y[row] = W[row] . x
-__global__ void __launch_bounds__(64) k_matvec_f32(const float* W, long long ldw, const float* x, float* y, int N,
-                                                  int K) {
-    const int row = blockIdx.x, lane = threadIdx.x;
-    if (row >= N) return;
+// Decode: one 256-thread workgroup per row, 16-byte loads all issued up front (K / 1024 per thread), x
+// re-read from L1 / L2. y[row] = W[row] . x
+__device__ __forceinline__ float block256_sum(float v, float* part) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float s = (part[0] + part[1]) + (part[2] + part[3]);
+    __syncthreads();
+    return s;
+}
+
+__global__ void __launch_bounds__(256) k_matvec_f32(const float* W, long long ldw, const float* x, float* y, int N,
+                                                   int K) {
+    __shared__ float part[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
     const float* wr = W + (size_t)row * ldw;
     float acc = 0.0f;
     if ((K & 3) == 0 && (((uintptr_t)wr | (uintptr_t)x) & 15) == 0) {
         const float4* w4 = (const float4*)wr;
         const float4* x4 = (const float4*)x;
-        for (int i = lane; i < K / 4; i += 64) {
+#pragma unroll 4
+        for (int i = tid; i < K / 4; i += 256) {
             const float4 a = w4[i], b = x4[i];
             acc = fmaf(a.x, b.x, acc);
             acc = fmaf(a.y, b.y, acc);
@@ -148,10 +159,10 @@ __global__ void __launch_bounds__(64) k_matvec_f32(const float* W, long long ldw
             acc = fmaf(a.w, b.w, acc);
         }
     } else {
-        for (int i = lane; i < K; i += 64) acc = fmaf(wr[i], x[i], acc);
+        for (int i = tid; i < K; i += 256) acc = fmaf(wr[i], x[i], acc);
     }
-    acc = wave_sum(acc);
-    if (lane == 0) y[row] = acc;
+    acc = block256_sum(acc, part);
+    if (tid == 0) y[row] = acc;
 }
 
 // Prefill: tiles of 64 tokens x 64 rows, K staged through LDS in chunks of 32; each thread 4 x 4 outputs.
@@ -197,81 +208,68 @@ __global__ void __launch_bounds__(256) k_matmul_f32(const float* W, long long ld
 
 // ------------------------------------------------------------------ router (src/gpu_ops.hip:185-241)
 
-// One wave per token. Lane l holds the logits of experts l + 64 j (j < PL) in registers. The selection runs
-// n_used rounds of a wave arg-max on the logits (softmax is strictly monotonic, so this is the order of the
-// probabilities), ties to the lower expert index; the selected probabilities exp(l - max) / sum are then
-// renormalised by max(sum of them, 6.103515625e-5).
-template <int PL>
-__global__ void __launch_bounds__(64) k_router(const float* logits, const float* x, const float* w_shexp, int* ids,
-                                               float* wts, float* sg, int ne, int nu, int n, int ids_stride) {
+// One 256-thread workgroup per token. The logits go to LDS; softmax max and sum by DPP wave reductions. The
+// selection ranks every expert by counting the experts that beat it (a larger logit, or an equal one at a lower
+// index): softmax is strictly monotonic, so this is the order of the probabilities, ties to the lower index,
+// and the experts of rank < n_used are the selection in descending order. Every count reads the same LDS
+// address across the wave (a broadcast), with no cross-lane dependency chain. The selected probabilities
+// exp(l - max) / sum are renormalised by max(their sum, 6.103515625e-5), summed in rank order.
+#define ROUTER_MAX_E 1024
+__global__ void __launch_bounds__(256) k_router(const float* logits, const float* x, const float* w_shexp, int* ids,
+                                                float* wts, float* sg, int ne, int nu, int n, int ids_stride) {
+    __shared__ __attribute__((aligned(16))) float sl[ROUTER_MAX_E];
+    __shared__ float part[4];
     __shared__ float sel_p[64];
-    const int t = blockIdx.x, lane = threadIdx.x;
+    const int t = blockIdx.x, tid = threadIdx.x;
     const float* lg = logits + (size_t)t * ne;
+    for (int e = tid; e < ne; e += 256) sl[e] = lg[e];
+    const int ne4 = (ne + 3) & ~3;
+    for (int e = ne + tid; e < ne4; e += 256) sl[e] = -INFINITY;  // pad: never beats a real expert
 
     if (w_shexp) {  // the shared-expert gate (uniform branch)
         const float* xr = x + (size_t)t * n;
         float d = 0.0f;
         if ((n & 3) == 0 && (((uintptr_t)xr | (uintptr_t)w_shexp) & 15) == 0) {
-            for (int i = lane; i < n / 4; i += 64) {
+            for (int i = tid; i < n / 4; i += 256) {
                 const float4 a = ((const float4*)xr)[i], b = ((const float4*)w_shexp)[i];
                 d += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
             }
         } else {
-            for (int i = lane; i < n; i += 64) d += xr[i] * w_shexp[i];
+            for (int i = tid; i < n; i += 256) d += xr[i] * w_shexp[i];
         }
-        d = wave_sum(d);
-        if (lane == 0) sg[t] = 1.0f / (1.0f + expf(-d));
+        d = block256_sum(d, part);
+        if (tid == 0) sg[t] = 1.0f / (1.0f + expf(-d));
     }
 
-    float v[PL];
     float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < PL; ++j) {
-        const int e = lane + 64 * j;
-        v[j] = e < ne ? lg[e] : -INFINITY;
-        mx = fmaxf(mx, v[j]);
-    }
+    for (int e = tid; e < ne; e += 256) mx = fmaxf(mx, lg[e]);
     mx = wave_max(mx);
+    if ((tid & 63) == 0) part[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+    __syncthreads();
     float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < PL; ++j)
-        if (lane + 64 * j < ne) sum += expf(v[j] - mx);
-    sum = wave_sum(sum);
+    for (int e = tid; e < ne; e += 256) sum += expf(sl[e] - mx);
+    sum = block256_sum(sum, part);
     const float inv = 1.0f / sum;
 
     int* id_row = ids + (size_t)t * ids_stride;
-    for (int r = 0; r < nu; ++r) {
-        float bv = v[0];
-        int bj = 0;
-#pragma unroll
-        for (int j = 1; j < PL; ++j)
-            if (v[j] > bv) {
-                bv = v[j];
-                bj = j;
-            }
-        int be = lane + 64 * bj;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(bv, off, 64);
-            const int oe = __shfl_xor(be, off, 64);
-            if (ov > bv || (ov == bv && oe < be)) {
-                bv = ov;
-                be = oe;
-            }
+    for (int e = tid; e < ne; e += 256) {  // uniform trip count per wave except the last
+        const float v = sl[e];
+        int rank = 0;
+        for (int k = 0; k < ne4; k += 4) {
+            const float4 c = *(const float4*)(sl + k);
+            rank += (c.x > v || (c.x == v && k < e)) + (c.y > v || (c.y == v && k + 1 < e)) +
+                    (c.z > v || (c.z == v && k + 2 < e)) + (c.w > v || (c.w == v && k + 3 < e));
         }
-        if (lane == 0) {
-            id_row[r] = be;
-            sel_p[r] = expf(bv - mx) * inv;
-        }
-        if ((be & 63) == lane) {
-#pragma unroll
-            for (int j = 0; j < PL; ++j)
-                if (j == (be >> 6)) v[j] = -INFINITY;
+        if (rank < nu) {
+            id_row[rank] = e;
+            sel_p[rank] = expf(v - mx) * inv;
         }
     }
-    if (lane == 0 && ids_stride > nu) id_row[nu] = -1;
+    if (tid == 0 && ids_stride > nu) id_row[nu] = -1;
     __syncthreads();
-    if (lane == 0) {
+    if (tid == 0) {
         float ws = 0.0f;
         for (int r = 0; r < nu; ++r) ws += sel_p[r];
         ws = fmaxf(ws, 6.103515625e-5f);
@@ -320,7 +318,7 @@ extern "C" hipError_t qmatvec_launch(int type, const void* W, size_t row_bytes, 
     if (!moe_lib_ready()) return hipErrorNotInitialized;
     if (type != QT_F32) return hipErrorInvalidDeviceFunction;
     if (N <= 0 || K <= 0 || row_bytes != (size_t)K * 4) return hipErrorInvalidValue;
-    return launch_kernel(k_matvec_f32, dim3(N), dim3(64), 0, stream, (const float*)W, (long long)K, x, y, N, K);
+    return launch_kernel(k_matvec_f32, dim3(N), dim3(256), 0, stream, (const float*)W, (long long)K, x, y, N, K);
 }
 
 extern "C" hipError_t qmatvec_launch_batch(int type, const void* W, size_t row_bytes, const float* x, float* y, int N,
@@ -356,21 +354,8 @@ extern "C" hipError_t gpu_moe_router(const float* logits, const float* x, const 
         return hipErrorInvalidValue;
     if (ids_stride == 0) ids_stride = n_used;
     if (ids_stride < n_used || (w_shexp && (!x || !sg || n <= 0))) return hipErrorInvalidValue;
-    const dim3 g(T), b(64);
-    if (n_expert <= 64)
-        return launch_kernel(k_router<1>, g, b, 0, stream, logits, x, w_shexp, ids, wts, sg, n_expert, n_used, n,
-                             ids_stride);
-    if (n_expert <= 128)
-        return launch_kernel(k_router<2>, g, b, 0, stream, logits, x, w_shexp, ids, wts, sg, n_expert, n_used, n,
-                             ids_stride);
-    if (n_expert <= 256)
-        return launch_kernel(k_router<4>, g, b, 0, stream, logits, x, w_shexp, ids, wts, sg, n_expert, n_used, n,
-                             ids_stride);
-    if (n_expert <= 512)
-        return launch_kernel(k_router<8>, g, b, 0, stream, logits, x, w_shexp, ids, wts, sg, n_expert, n_used, n,
-                             ids_stride);
-    return launch_kernel(k_router<16>, g, b, 0, stream, logits, x, w_shexp, ids, wts, sg, n_expert, n_used, n,
-                         ids_stride);
+    return launch_kernel(k_router, dim3(T), dim3(256), 0, stream, logits, x, w_shexp, ids, wts, sg, n_expert, n_used,
+                         n, ids_stride);
 }
 
 extern "C" hipError_t gpu_moe_combine_scaled(const float* down, const float* wts, const float* shared, const float* sg,
