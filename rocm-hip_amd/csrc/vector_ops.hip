@@ -146,6 +146,8 @@ __global__ void __launch_bounds__(256) k_matvec_f32(const float* W, long long ld
     __shared__ float part[4];
     const int row = blockIdx.x, tid = threadIdx.x;
     const float* wr = W + (size_t)row * ldw;
+    x += (size_t)blockIdx.y * K;  // token
+    y += (size_t)blockIdx.y * N;
     float acc = 0.0f;
     if ((K & 3) == 0 && (((uintptr_t)wr | (uintptr_t)x) & 15) == 0) {
         const float4* w4 = (const float4*)wr;
@@ -165,18 +167,19 @@ __global__ void __launch_bounds__(256) k_matvec_f32(const float* W, long long ld
     if (tid == 0) y[row] = acc;
 }
 
-// Prefill: tiles of 64 tokens x 64 rows, K staged through LDS in chunks of 32; each thread 4 x 4 outputs.
-#define MF_TT 64
-#define MF_TR 64
-#define MF_KC 32
+// Prefill: tiles of 32 tokens x 32 rows (enough workgroups to fill the chip at a few thousand tokens), K staged
+// through LDS in chunks of 64; each thread 2 x 2 outputs.
+#define MF_TT 32
+#define MF_TR 32
+#define MF_KC 64
 __global__ void __launch_bounds__(256) k_matmul_f32(const float* W, long long ldw, const float* X, float* Y, int N,
                                                    int K, int T) {
-    __shared__ float sw[MF_KC][MF_TR + 4];
-    __shared__ float sx[MF_KC][MF_TT + 4];
+    __shared__ float sw[MF_KC][MF_TR + 1];
+    __shared__ float sx[MF_KC][MF_TT + 1];
     const int tid = threadIdx.x;
     const int r0 = blockIdx.x * MF_TR, t0 = blockIdx.y * MF_TT;
-    const int tr = (tid & 15) * 4, tt = (tid >> 4) * 4;
-    float acc[4][4] = {};
+    const int tr = (tid & 15) * 2, tt = (tid >> 4) * 2;
+    float acc[2][2] = {};
     for (int k0 = 0; k0 < K; k0 += MF_KC) {
         for (int i = tid; i < MF_TR * MF_KC; i += 256) {
             const int r = i / MF_KC, k = i % MF_KC;
@@ -184,25 +187,20 @@ __global__ void __launch_bounds__(256) k_matmul_f32(const float* W, long long ld
             sx[k][r] = (t0 + r < T && k0 + k < K) ? X[(size_t)(t0 + r) * K + k0 + k] : 0.0f;
         }
         __syncthreads();
-#pragma unroll 8
+#pragma unroll 16
         for (int k = 0; k < MF_KC; ++k) {
-            float a[4], b[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                a[j] = sx[k][tt + j];
-                b[j] = sw[k][tr + j];
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+            const float a0 = sx[k][tt], a1 = sx[k][tt + 1], b0 = sw[k][tr], b1 = sw[k][tr + 1];
+            acc[0][0] = fmaf(a0, b0, acc[0][0]);
+            acc[0][1] = fmaf(a0, b1, acc[0][1]);
+            acc[1][0] = fmaf(a1, b0, acc[1][0]);
+            acc[1][1] = fmaf(a1, b1, acc[1][1]);
         }
         __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 2; ++j)
             if (t0 + tt + i < T && r0 + tr + j < N) Y[(size_t)(t0 + tt + i) * N + r0 + tr + j] = acc[i][j];
 }
 
@@ -326,7 +324,8 @@ extern "C" hipError_t qmatvec_launch_batch(int type, const void* W, size_t row_b
     if (!moe_lib_ready()) return hipErrorNotInitialized;
     if (type != QT_F32) return hipErrorInvalidDeviceFunction;
     if (N <= 0 || K <= 0 || T <= 0 || row_bytes != (size_t)K * 4) return hipErrorInvalidValue;
-    if (T == 1) return qmatvec_launch(type, W, row_bytes, x, y, N, K, stream);
+    if (T <= 16)  // a few tokens: the decode kernel per token (the same sums as T single-token launches)
+        return launch_kernel(k_matvec_f32, dim3(N, T), dim3(256), 0, stream, (const float*)W, (long long)K, x, y, N, K);
     return launch_kernel(k_matmul_f32, dim3((N + MF_TR - 1) / MF_TR, (T + MF_TT - 1) / MF_TT), dim3(256), 0, stream,
                          (const float*)W, (long long)K, x, y, N, K, T);
 }
