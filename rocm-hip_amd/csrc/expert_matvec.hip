@@ -529,7 +529,7 @@ extern "C" hipError_t qmatvec_launch_q8_batch(int type, const void* W, size_t ro
 // Entry tiles of the grouped kernels (the MFMA kernel's 64; the per-entry fallback takes any)
 #define ENTRY_TILE 64
 
-bool moe_grouped_mfma_type(int type);
+bool moe_grouped_mfma_ok(int type, int N, int K);
 hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
                                    const qmatvec_q8* q, float* y, int N, int K, int max_tiles, const int32_t* n_tiles,
                                    const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
@@ -582,7 +582,7 @@ extern "C" hipError_t qmatvec_launch_q8_id_batch(int type, const void* W, size_t
     if (!qmatvec_q8_supported(type, K)) return hipErrorInvalidDeviceFunction;
     if (!W || !q || row_bytes != native_row(type, K) || !aligned(W, 4)) return hipErrorInvalidValue;
     const uint8_t *v = nullptr, *s = nullptr;
-    if (moe_grouped_mfma_type(type) && find_packed(W, type, K, row_bytes, &v, &s))
+    if (moe_grouped_mfma_ok(type, N, K) && find_packed(W, type, K, row_bytes, &v, &s))
         return moe_launch_grouped_mfma(type, v, s, fmt_value_row(type, K), fmt_scale_row(type, K), q, y, N, K,
                                        max_tiles, n_tiles, tile_e, tile_start, tile_n, in_rows, out_rows, stream);
     return moe_launch_entries(type, W, row_bytes, q, y, N, K, max_tiles, n_tiles, tile_e, tile_start, tile_n, in_rows,

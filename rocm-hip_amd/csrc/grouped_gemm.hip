@@ -55,122 +55,156 @@ __device__ __forceinline__ void acc_block(v16f& acc, const v16i& I, const v16f& 
     for (int j = 0; j < 16; ++j) acc[j] = fmaf((float)I[j], S[j], acc[j]);
 }
 
-// The A operand (16 int8 codes, K half kh) of a 32-value block for one weight row, and the block's scale(s)
+// ---- Pipeline. K runs in stages of GG_KB blocks through one LDS buffer per workgroup (about 25 KB, so several
+// workgroups share a CU and hide each other's load latency). All operand bytes move from memory to LDS with
+// global_load_lds_dwordx4 (no register staging): lane l of such a load writes its 16 bytes to slot l of a 1 KB
+// LDS run, so each load is laid out to be read back as an MFMA operand with one ds_read per lane:
+//   weights: per wave and block, lane l loads row (l % 32) of the wave's 32 rows, K half l / 32 (Q8_0), or the
+//            block's 16 nibble bytes of that row (FP4 types: the lane decodes its K half from them);
+//   activations: per block and 32-entry tile, lane l loads entry (l % 32), K half l / 32;
+//   activation scales: one 16-byte load per entry (GG_KB floats).
+// The weight rows' scale bytes come through registers.
+#define GG_KB 4                          // blocks of 32 values per stage
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+struct GBuf {  // one stage of operands
+    uint8_t a[4][GG_KB][1024];  // [wave][block][lane * 16]
+    uint8_t b[GG_KB][2][1024];  // [block][entry tile][lane * 16]
+    float dx[GG_TILE][GG_KB];   // [entry][block]
+};
+
+__device__ __forceinline__ void lds_load16(const void* g, void* lds_run) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_run, 16, 0, 0);
+}
+
+template <int WAITS>
+__device__ __forceinline__ void wait_vm() {
+    // s_waitcnt vmcnt(WAITS), expcnt and lgkmcnt left at their maxima (gfx9 encoding)
+    __builtin_amdgcn_s_waitcnt((WAITS & 0xf) | ((WAITS >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// Issue one stage's loads into B (see above); the weight scales of the stage go to wsc
 template <int TYPE>
-struct BlockA;
-
-template <>
-struct BlockA<QT_Q8_0> {
-    v4i a;
-    float d;
-    __device__ __forceinline__ void load(const uint8_t* vrow, const uint8_t* srow, int b, int nb, int kh) {
-        a = *(const v4i*)(vrow + 16 * (kh ? nb + b : b));
-        d = h2f(*(const uint16_t*)(srow + 2 * b));
-    }
-};
-
-template <>
-struct BlockA<QT_ROCMFP4_FAST> {
-    v4i a;
-    float d;
-    __device__ __forceinline__ void load(const uint8_t* vrow, const uint8_t* srow, int b, int nb, int kh) {
-        const uint4 q = *(const uint4*)(vrow + 16 * b);  // values j: low nibble of byte j, j + 16: high nibble
-        const uint32_t sh = kh ? 4 : 0;
-        a[0] = (int)fp4x4_to_i8x4(q.x >> sh);
-        a[1] = (int)fp4x4_to_i8x4(q.y >> sh);
-        a[2] = (int)fp4x4_to_i8x4(q.z >> sh);
-        a[3] = (int)fp4x4_to_i8x4(q.w >> sh);
-        d = ue4m3_half(srow[b]);
-    }
-};
-
-// ROCmFP4: two 16-value halves with their own scales; K half kh of half h is values 16 h + 8 kh .. + 7, i.e.
-// the low (h = 0) or high (h = 1) nibbles of value bytes 8 kh .. 8 kh + 7
-struct BlockA4 {
-    long a[2];
-    float e[2];
-    __device__ __forceinline__ void load(const uint8_t* vrow, const uint8_t* srow, int b, int kh) {
-        const uint2 q = *(const uint2*)(vrow + 16 * b + 8 * kh);
-        const uint32_t lo0 = fp4x4_to_i8x4(q.x), lo1 = fp4x4_to_i8x4(q.y);
-        const uint32_t hi0 = fp4x4_to_i8x4(q.x >> 4), hi1 = fp4x4_to_i8x4(q.y >> 4);
-        a[0] = (long)(((unsigned long)lo1 << 32) | lo0);
-        a[1] = (long)(((unsigned long)hi1 << 32) | hi0);
-        const uint32_t ee = *(const uint16_t*)(srow + 2 * b);
-        e[0] = ue4m3_half(ee & 0xffu);
-        e[1] = ue4m3_half(ee >> 8);
-    }
-};
-
-template <int TYPE>
-__global__ void __launch_bounds__(256) k_grouped_mfma(GArgs a) {
-    const int k = blockIdx.y;
-    if (k >= *a.n_tiles) return;
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, lr = l & 31, kh = l >> 5;
-    const int r0 = blockIdx.x * GG_ROWS + w * 32;
-    if (r0 >= a.N) return;  // (uniform per wave)
-    const int e = a.tile_e[k], st = a.tile_start[k], cnt = a.tile_n[k];
-    const bool two = cnt > 32;
-    const int row = min(r0 + lr, a.N - 1);
-    const long long grow = (long long)e * a.N + row;
-    const uint8_t* vrow = a.v + grow * a.vrb;
-    const uint8_t* srow = a.s + grow * a.srb;
-    const int K = a.K, nb = K / 32;
-    const long long in0 = a.in_rows[st + min(lr, cnt - 1)], in1 = a.in_rows[st + min(32 + lr, cnt - 1)];
-    const int8_t* x0 = a.xq + in0 * K;
-    const int8_t* x1 = a.xq + in1 * K;
-    const float* d0 = a.xd + in0 * nb;
-    const float* d1 = a.xd + in1 * nb;
-    v16f acc0 = {}, acc1 = {};
-    const v16i zi = {};
-    for (int b = 0; b < nb; ++b) {
-        if constexpr (TYPE == QT_ROCMFP4) {
-            BlockA4 A;
-            A.load(vrow, srow, b, kh);
+__device__ __forceinline__ void g_issue(GBuf& B, int b0, uint4& wsc, const uint8_t* vrow, const uint8_t* srow,
+                                        const int8_t* xrow, const float* dxr, int nb, int w, int l, int kh,
+                                        int tile_b) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const long b0 = *(const long*)(x0 + 32 * b + 16 * h + 8 * kh);
-                const v16i I0 = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.a[h], b0, zi, 0, 0, 0);
-                acc_block(acc0, I0, scale_outer(A.e[h], d0[b], kh));
-                if (two) {
-                    const long b1 = *(const long*)(x1 + 32 * b + 16 * h + 8 * kh);
-                    const v16i I1 = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.a[h], b1, zi, 0, 0, 0);
-                    acc_block(acc1, I1, scale_outer(A.e[h], d1[b], kh));
-                }
-            }
-        } else {
-            BlockA<TYPE> A;
-            A.load(vrow, srow, b, nb, kh);
-            const v4i b0 = *(const v4i*)(x0 + 32 * b + 16 * kh);
-            const v16i I0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A.a, b0, zi, 0, 0, 0);
-            acc_block(acc0, I0, scale_outer(A.d, d0[b], kh));
-            if (two) {
-                const v4i b1 = *(const v4i*)(x1 + 32 * b + 16 * kh);
-                const v16i I1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A.a, b1, zi, 0, 0, 0);
-                acc_block(acc1, I1, scale_outer(A.d, d1[b], kh));
-            }
-        }
+    for (int bb = 0; bb < GG_KB; ++bb) {
+        const uint8_t* g = TYPE == QT_Q8_0 ? vrow + 16 * (kh ? nb + b0 + bb : b0 + bb) : vrow + 16 * (b0 + bb);
+        lds_load16(g, B.a[w][bb]);
     }
-    // acc[j] is C[row 8 (j / 4) + 4 kh + j % 4][entry lr] of the wave's 32 x 32 tile
-    if (lr < cnt) {
-        float* y = a.y + (long long)a.out_rows[st + lr] * a.N;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int ri = r0 + 8 * (j >> 2) + 4 * kh + (j & 3);
-            if (ri < a.N) y[ri] = acc0[j];
-        }
+    for (int j = 0; j < GG_KB / 2; ++j) {
+        const int bb = (w >> 1) + 2 * j;
+        lds_load16(xrow + 32 * (b0 + bb), B.b[bb][tile_b]);
     }
-    if (two && 32 + lr < cnt) {
-        float* y = a.y + (long long)a.out_rows[st + 32 + lr] * a.N;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int ri = r0 + 8 * (j >> 2) + 4 * kh + (j & 3);
-            if (ri < a.N) y[ri] = acc1[j];
-        }
+    if (l < 16) lds_load16(dxr + b0, &B.dx[16 * w][0]);  // entries 16 w + l (lanes 16.. idle)
+    if constexpr (TYPE == QT_ROCMFP4_FAST) {
+        wsc = make_uint4(*(const uint32_t*)(srow + b0), 0u, 0u, 0u);
+    } else {
+        const uint2 v = *(const uint2*)(srow + 2 * b0);
+        wsc = make_uint4(v.x, v.y, 0u, 0u);
     }
 }
 
-// Whether the MFMA kernel takes this matrix: a split-plane type with Q8_0 activations
-bool moe_grouped_mfma_type(int type) { return type == QT_Q8_0 || type == QT_ROCMFP4 || type == QT_ROCMFP4_FAST; }
+// The MFMAs of one stage from B
+template <int TYPE>
+__device__ __forceinline__ void g_compute(const GBuf& B, const uint4& wsc, v16f& acc0, v16f& acc1, int w, int l,
+                                          int lr, int kh) {
+    const v16i zi = {};
+#pragma unroll
+    for (int bb = 0; bb < GG_KB; ++bb) {
+        const float dx0 = B.dx[lr][bb], dx1 = B.dx[32 + lr][bb];
+        const uint8_t* arun = B.a[w][bb] + 16 * l;
+        if constexpr (TYPE == QT_ROCMFP4) {
+            const uint2 q = *(const uint2*)(arun + 8 * kh);  // bytes 8 kh .. 8 kh + 7 of the row's block
+            const uint32_t ew = (bb < 2 ? wsc.x : wsc.y) >> (16 * (bb & 1));
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t sh = 4 * h;
+                const long A = (long)(((unsigned long)fp4x4_to_i8x4(q.y >> sh) << 32) | fp4x4_to_i8x4(q.x >> sh));
+                const float ee = ue4m3_half((ew >> (8 * h)) & 0xffu);
+                // B, K half kh of 16-value half h: bytes 16 h + 8 kh of the block = 8 bytes of the slot of the
+                // lane that loaded (entry, K half h)
+                const long B0 = *(const long*)(B.b[bb][0] + 16 * (lr + 32 * h) + 8 * kh);
+                const long B1 = *(const long*)(B.b[bb][1] + 16 * (lr + 32 * h) + 8 * kh);
+                acc_block(acc0, __builtin_amdgcn_mfma_i32_32x32x16_i8(A, B0, zi, 0, 0, 0), scale_outer(ee, dx0, kh));
+                acc_block(acc1, __builtin_amdgcn_mfma_i32_32x32x16_i8(A, B1, zi, 0, 0, 0), scale_outer(ee, dx1, kh));
+            }
+        } else {
+            const uint4 q = *(const uint4*)arun;
+            v4i A;
+            float dw;
+            if constexpr (TYPE == QT_Q8_0) {
+                A = (v4i){(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+                dw = h2f((uint16_t)((bb < 2 ? wsc.x : wsc.y) >> (16 * (bb & 1))));
+            } else {  // FAST: K half kh = the low (0) or high (1) nibbles of the block's 16 bytes
+                const uint32_t sh = kh ? 4 : 0;
+                A = (v4i){(int)fp4x4_to_i8x4(q.x >> sh), (int)fp4x4_to_i8x4(q.y >> sh), (int)fp4x4_to_i8x4(q.z >> sh),
+                          (int)fp4x4_to_i8x4(q.w >> sh)};
+                dw = ue4m3_half((wsc.x >> (8 * bb)) & 0xffu);
+            }
+            const v4i B0 = *(const v4i*)(B.b[bb][0] + 16 * l);
+            const v4i B1 = *(const v4i*)(B.b[bb][1] + 16 * l);
+            acc_block(acc0, __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B0, zi, 0, 0, 0), scale_outer(dw, dx0, kh));
+            acc_block(acc1, __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B1, zi, 0, 0, 0), scale_outer(dw, dx1, kh));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <int TYPE>
+__global__ void __launch_bounds__(256) k_grouped_mfma(GArgs a) {
+    __shared__ __attribute__((aligned(1024))) GBuf buf;
+    const int k = blockIdx.y;
+    if (k >= *a.n_tiles) return;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lr = l & 31, kh = l >> 5;
+    const int e = a.tile_e[k], st = a.tile_start[k];
+    const int cnt = __builtin_amdgcn_readfirstlane(a.tile_n[k]);
+    const int K = a.K, nb = K / 32;
+    // this lane's weight row (the launcher requires N % 128 == 0 and K % (32 GG_KB) == 0)
+    const int r0 = blockIdx.x * GG_ROWS + 32 * w;
+    const long long grow = (long long)e * a.N + r0 + lr;
+    const uint8_t* vrow = a.v + grow * a.vrb;
+    const uint8_t* srow = a.s + grow * a.srb;
+    // activation loads: this wave loads blocks (w >> 1) and (w >> 1) + 2 of tile (w & 1), entry 32 (w & 1) + lr
+    const int tile_b = w & 1;
+    const int8_t* xrow = a.xq + (long long)a.in_rows[st + min(32 * tile_b + lr, cnt - 1)] * K + 16 * kh;
+    // activation scales: this wave's lanes 0..15 load entries 16 w + l
+    const float* dxr = a.xd + (long long)a.in_rows[st + min(16 * w + (l & 15), cnt - 1)] * nb;
+
+    v16f acc0 = {}, acc1 = {};
+    const int nst = nb / GG_KB;
+    uint4 wsc;
+    for (int s = 0; s < nst; ++s) {
+        // one stage: its loads, then (with several workgroups per CU hiding the latency of each other's loads)
+        // its MFMAs
+        g_issue<TYPE>(buf, s * GG_KB, wsc, vrow, srow, xrow, dxr, nb, w, l, kh, tile_b);
+        wait_vm<0>();
+        __syncthreads();
+        g_compute<TYPE>(buf, wsc, acc0, acc1, w, l, lr, kh);
+        __syncthreads();
+    }
+    // acc[j] is C[row 8 (j / 4) + 4 kh + j % 4][entry lr] of the wave's 32 x 32 tile
+    if (lr < cnt) {
+        float* y = a.y + (long long)a.out_rows[st + lr] * a.N + r0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) y[8 * (j >> 2) + 4 * kh + (j & 3)] = acc0[j];
+    }
+    if (32 + lr < cnt) {
+        float* y = a.y + (long long)a.out_rows[st + 32 + lr] * a.N + r0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) y[8 * (j >> 2) + 4 * kh + (j & 3)] = acc1[j];
+    }
+}
+
+// Whether the MFMA kernel takes this matrix: a split-plane type with Q8_0 activations, whole 128-row blocks and
+// whole 4-block K stages
+bool moe_grouped_mfma_ok(int type, int N, int K) {
+    return (type == QT_Q8_0 || type == QT_ROCMFP4 || type == QT_ROCMFP4_FAST) && N % GG_ROWS == 0 &&
+           K % (GG_KB * 32) == 0;
+}
 
 hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
                                    const qmatvec_q8* q, float* y, int N, int K, int max_tiles, const int32_t* n_tiles,
