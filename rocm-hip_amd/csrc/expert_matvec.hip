@@ -32,59 +32,6 @@ struct MvArgs {
     int N, N2, K;
 };
 
-template <int TYPE, bool PACKED>
-__device__ __forceinline__ void load_unit(const uint8_t* vrow, const uint8_t* srow, int u, int nu, WUnit<TYPE>& w) {
-    if constexpr (PACKED)
-        load_packed<TYPE>(vrow, srow, u, nu, w);
-    else
-        load_native<TYPE>(vrow, u, w);
-}
-
-// R rows (row0 + r * stride) of the matrix at (vbase, sbase) against one input row; returns the group sums.
-// NUPL > 0: every lane has exactly NUPL units (nu == NUPL * L) and all R * NUPL weight loads (and the NUPL
-// activation loads) are issued before any arithmetic; NUPL == 0: a loop over the lane's units.
-template <int TYPE, bool PACKED, int L, int R, int NUPL>
-__device__ __forceinline__ void rows_dot(const uint8_t* vbase, const uint8_t* sbase, long long vrb, long long srb,
-                                         int row0, int stride, int nrows, const int8_t* xq, const float* xd,
-                                         const int* xbs, int K, int gl, float acc[R]) {
-    const int nu = fmt_units(TYPE, K);
-    const uint8_t* vr[R];
-    const uint8_t* sr[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int row = min(row0 + r * stride, nrows - 1);  // rows past the end load a valid row, unused
-        vr[r] = vbase + (long long)row * vrb;
-        sr[r] = PACKED ? sbase + (long long)row * srb : nullptr;
-        acc[r] = 0.0f;
-    }
-    if constexpr (NUPL > 0) {
-        WUnit<TYPE> w[NUPL][R];
-        XUnit<TYPE> x[NUPL];
-#pragma unroll
-        for (int i = 0; i < NUPL; ++i)
-#pragma unroll
-            for (int r = 0; r < R; ++r) load_unit<TYPE, PACKED>(vr[r], sr[r], gl + i * L, nu, w[i][r]);
-#pragma unroll
-        for (int i = 0; i < NUPL; ++i) load_x<TYPE>(xq, xd, xbs, gl + i * L, x[i]);
-#pragma unroll
-        for (int i = 0; i < NUPL; ++i)
-#pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] += term<TYPE>(w[i][r], x[i], gl + i * L);
-    } else {
-        for (int u = gl; u < nu; u += L) {
-            XUnit<TYPE> x;
-            load_x<TYPE>(xq, xd, xbs, u, x);
-            WUnit<TYPE> w[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) load_unit<TYPE, PACKED>(vr[r], sr[r], u, nu, w[r]);
-#pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] += term<TYPE>(w[r], x, u);
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = group_sum<L>(acc[r]);
-}
-
 template <int TYPE>
 __device__ __forceinline__ void act_row(const MvArgs& a, long long in_row, const int8_t*& xq, const float*& xd,
                                         const int*& xbs) {
@@ -423,6 +370,18 @@ extern "C" void qmatvec_unpack_weights(const void* W) {
     }
     // launches already queued on any stream may still read the copy
     if (hipDeviceSynchronize() == hipSuccess) (void)hipFree(mem);
+}
+
+// The per-operation kernels' lane shape for a row of K values (the fused layer kernel copies it)
+void moe_mv_shape(int type, int K, int* lanes, int* units_per_lane) {
+    const MvShape sh = mv_shape(type, K);
+    *lanes = sh.L;
+    *units_per_lane = sh.nupl;
+}
+
+// The split-plane rows of the registered matrix at W (for the fused layer kernel)
+bool moe_packed_planes(const void* W, int type, int K, size_t row_bytes, const uint8_t** v, const uint8_t** s) {
+    return find_packed(W, type, K, row_bytes, v, s);
 }
 
 // Drop every registration (library teardown)

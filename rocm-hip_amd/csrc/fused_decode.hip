@@ -1,0 +1,358 @@
+// fused_decode.hip -- one batch-1 MoE FFN layer in one persistent kernel (gfx950, wave64).
+//
+// The multi-kernel layer (router logits, router, quantize, gate/up, SwiGLU, down, combine) costs seven launches,
+// each with ~2.5 us of ramp and tail on MI355X, while the layer's ~25-40 MB of weights take 3-5 us at HBM speed.
+// Here one grid of one workgroup per CU runs the layer in three phases separated by two grid barriers:
+//   A  every workgroup quantizes x into LDS (the activation quantizer's exact expressions); the router-logit
+//      rows are spread over the workgroups; one workgroup computes the shared-expert gate;
+//   B  every workgroup routes (the router's own code on the logits), then works through units of (slot, 32-row
+//      block of FE): the 32 gate rows and 32 up rows of the slot's expert, SwiGLU, and the Q8_0 quantization of
+//      those 32 values, which are one Q8_0 block of the down projection's input;
+//   C  units of 8 output rows: their down rows for every slot, then the combine in slot order.
+// Every sum is formed in the same order as the per-operation kernels (rows_dot's lane groups and DPP group sums,
+// the same router, quantizer and combine), so the layer's output equals moe_layer_forward's multi-kernel path
+// bit for bit.
+//
+// The barriers spin on a generation word with a bounded wait: a barrier that does not complete (the grid not
+// co-resident) sets an error word and the kernel exits instead of hanging. The barrier words live in the
+// caller's scratch, zero before the first launch and zero again after every completed launch.
+
+#include "expert_units.h"
+#include "host_common.h"
+#include "moe_layer.h"
+#include "qmatvec.h"
+#include "router_dev.h"
+
+#define FD_MAX_E 4096
+#define FD_RB 8                 // output rows per down unit
+#define FD_SPIN_LIMIT (1u << 21)  // ~0.1 s of polling before a barrier gives up
+
+struct FArgs {
+    const float* x;          // [E]
+    const float* logits_in;  // [NE] or nullptr
+    const float* w_router;   // [NE][E]
+    const float* w_shexp;    // [E] or nullptr
+    const uint8_t* v[6];     // value planes: gate, up, down (stacked experts), shared gate, up, down
+    const uint8_t* s[6];     // scale planes
+    long long vrb_in, srb_in, vrb_out, srb_out;  // plane row bytes for K = E and K = FE
+    float* out;              // [E]
+    int* ids_out;            // [NU] or nullptr
+    float* wts_out;          // [NU] or nullptr
+    float* logits;           // scratch [NE]
+    float* sg;               // scratch [1]
+    int8_t* act_q;           // scratch [NS][FE]
+    float* act_d;            // scratch [NS][FE / 32]
+    unsigned* bar;           // scratch: count, generation, error
+    int E, NE, NU, FE, NS, has_gate;
+};
+
+// Grid barrier: the last arriving workgroup resets the count and bumps the generation. Agent-scope atomics and
+// fences make the phase's global writes visible across XCDs. Returns false after a timeout.
+__device__ __forceinline__ bool grid_sync(unsigned* bar, unsigned nblocks, int* flag) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned g0 = __hip_atomic_load(&bar[1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+        __threadfence();
+        const unsigned arrived = __hip_atomic_fetch_add(&bar[0], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        int ok = 1;
+        if (arrived == nblocks - 1) {
+            __hip_atomic_store(&bar[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(&bar[1], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            unsigned spins = 0;
+            while (__hip_atomic_load(&bar[1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == g0) {
+                __builtin_amdgcn_s_sleep(2);
+                if (++spins > FD_SPIN_LIMIT) {
+                    __hip_atomic_fetch_or(&bar[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ok = 0;
+                    break;
+                }
+            }
+        }
+        __threadfence();
+        *flag = ok;
+    }
+    __syncthreads();
+    return *flag != 0;
+}
+
+// The down phase's row dots: R row dots per lane group of L lanes, each with its own weight row and input row;
+// all loads first, then the units in ascending order per row (rows_dot's order), then the group sums
+template <int TYPE, int L, int R, int NUPL>
+__device__ __forceinline__ void rows_dot_multi(const uint8_t* const vr[R], const uint8_t* const sr[R],
+                                               const int8_t* const xq[R], const float* const xd[R], int nu, int gl,
+                                               float acc[R]) {
+    WUnit<TYPE> w[R][NUPL];
+    XUnit<TYPE> x[R][NUPL];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < NUPL; ++i) load_packed<TYPE>(vr[r], sr[r], gl + i * L, nu, w[r][i]);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < NUPL; ++i) load_x<TYPE>(xq[r], xd[r], nullptr, gl + i * L, x[r][i]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        acc[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NUPL; ++i) acc[r] += term<TYPE>(w[r][i], x[r][i], gl + i * L);
+        acc[r] = group_sum<L>(acc[r]);
+    }
+}
+
+template <int TYPE, int NUPL_IN, int L_OUT, int NUPL_OUT>
+__global__ void __launch_bounds__(256) k_fused_decode(FArgs a) {
+    __shared__ __attribute__((aligned(16))) int8_t sxq[FD_MAX_E];
+    __shared__ __attribute__((aligned(16))) float sxd[FD_MAX_E / 32];
+    __shared__ __attribute__((aligned(16))) float sl[ROUTER_MAX_E];
+    __shared__ float part[4];
+    __shared__ float sel_p[64];
+    __shared__ int s_ids[65];
+    __shared__ float s_wts[64];
+    __shared__ float gu[2][32];
+    __shared__ float downv[16][FD_RB];
+    __shared__ int flag;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const unsigned nb = gridDim.x;
+    const int E = a.E, FE = a.FE, NU = a.NU, NS = a.NS;
+
+    // ---- phase A: x quantized into LDS (Q8_0 per 32 values: 4 threads of 8 values), router logits, gate
+    for (int base = 0; base < E; base += 2048) {
+        const int i0 = base + 8 * tid;
+        float v[8];
+        float am = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v[j] = i0 + j < E ? a.x[i0 + j] : 0.0f;
+            am = fmaxf(am, fabsf(v[j]));
+        }
+        am = group_max<4>(am);
+        const float id = am != 0.0f ? 127.0f / am : 0.0f;
+        if (i0 < E) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) sxq[i0 + j] = (int8_t)(int)rintf(v[j] * id);
+            if ((tid & 3) == 0) sxd[i0 / 32] = __half2float(__float2half(am / 127.0f));
+        }
+    }
+    if (!a.logits_in)
+        for (int r = blockIdx.x; r < a.NE; r += nb) {
+            const float y = f32_row_dot(a.w_router + (size_t)r * E, a.x, E, part);
+            if (tid == 0) a.logits[r] = y;
+        }
+    if (a.has_gate && blockIdx.x == nb - 1) {
+        const float g = shexp_gate(a.x, a.w_shexp, E, part);
+        if (tid == 0) a.sg[0] = g;
+    }
+    if (!grid_sync(a.bar, nb, &flag)) return;
+
+    // ---- phase B: routing, then gate / up / SwiGLU / quantize per (slot, 32-row block)
+    router_select(a.logits_in ? a.logits_in : a.logits, a.NE, NU, sl, part, sel_p, s_ids, s_wts);
+    if (tid == 0) s_ids[NU] = -1;  // the shared expert's slot
+    __syncthreads();
+    if (blockIdx.x == 0 && tid < NU) {
+        if (a.ids_out) a.ids_out[tid] = s_ids[tid];
+        if (a.wts_out) a.wts_out[tid] = s_wts[tid];
+    }
+    const int nbf = FE / 32;
+    for (int u = blockIdx.x; u < NS * nbf; u += nb) {
+        const int slot = u / nbf, b = u - slot * nbf;
+        const int e = s_ids[slot];
+        const int mat = w >> 1;  // waves 0, 1: gate rows; 2, 3: up rows
+        const int mi = e >= 0 ? mat : 3 + mat;
+        const long long rbase = e >= 0 ? (long long)e * FE : 0;
+        const uint8_t* vb = a.v[mi] + rbase * a.vrb_in;
+        const uint8_t* sb = a.s[mi] + rbase * a.srb_in;
+        float acc[16];
+        rows_dot<TYPE, true, 64, 16, NUPL_IN>(vb, sb, a.vrb_in, a.srb_in, 32 * b + 16 * (w & 1), 1, FE, sxq, sxd,
+                                              nullptr, E, lane, acc);
+        if (lane == 0)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) gu[mat][16 * (w & 1) + r] = acc[r];
+        __syncthreads();
+        if (w == 0) {  // SwiGLU (the swiglu kernel's expression) and the Q8_0 block of these 32 values
+            const int t = lane & 31;
+            const float g = gu[0][t], uu = gu[1][t];
+            const float act = g / (1.0f + __expf(-g)) * uu;
+            const float am = group_max<32>(fabsf(act));
+            const float id = am != 0.0f ? 127.0f / am : 0.0f;
+            if (lane < 32) {
+                a.act_q[(long long)slot * FE + 32 * b + t] = (int8_t)(int)rintf(act * id);
+                if (t == 0) a.act_d[(long long)slot * nbf + b] = __half2float(__float2half(am / 127.0f));
+            }
+        }
+        __syncthreads();
+    }
+    if (!grid_sync(a.bar, nb, &flag)) return;
+
+    // ---- phase C: down rows of every slot for FD_RB output rows, then the combine in slot order. Lane groups of
+    // L_OUT lanes with NUPL_OUT units each: the per-operation down kernel's shape for this K, so the same sums.
+    const float sgv = a.has_gate ? a.sg[0] : 1.0f;
+    constexpr int NG = 256 / L_OUT;  // lane groups per workgroup
+    constexpr int RR = 4;            // row dots per group and round
+    const int gl = tid & (L_OUT - 1), grp = tid / L_OUT;
+    const int ndots = NS * FD_RB;
+    for (int t = blockIdx.x; t < E / FD_RB; t += nb) {
+        const int i0 = t * FD_RB;
+        for (int k0 = 0; k0 < ndots; k0 += NG * RR) {
+            const uint8_t* vr[RR];
+            const uint8_t* sr[RR];
+            const int8_t* xq[RR];
+            const float* xd[RR];
+#pragma unroll
+            for (int r = 0; r < RR; ++r) {
+                const int k = min(k0 + grp + NG * r, ndots - 1);  // idle row dots repeat the last one (not stored)
+                const int slot = k / FD_RB, i = k - slot * FD_RB;
+                const int e = s_ids[slot];
+                const long long row = e >= 0 ? (long long)e * E + i0 + i : i0 + i;
+                const int mi = e >= 0 ? 2 : 5;
+                vr[r] = a.v[mi] + row * a.vrb_out;
+                sr[r] = a.s[mi] + row * a.srb_out;
+                xq[r] = a.act_q + (long long)slot * FE;
+                xd[r] = a.act_d + (long long)slot * (FE / 32);
+            }
+            float acc[RR];
+            rows_dot_multi<TYPE, L_OUT, RR, NUPL_OUT>(vr, sr, xq, xd, FE / 32, gl, acc);
+            if (gl == 0)
+#pragma unroll
+                for (int r = 0; r < RR; ++r) {
+                    const int k = k0 + grp + NG * r;
+                    if (k < ndots) downv[k / FD_RB][k % FD_RB] = acc[r];
+                }
+        }
+        __syncthreads();
+        if (tid < FD_RB) {  // the combine kernel's expression
+            float o = s_wts[0] * downv[0][tid];
+            for (int j = 1; j < NU; ++j) o += s_wts[j] * downv[j][tid];
+            if (NS > NU) o += a.has_gate ? downv[NU][tid] * sgv : downv[NU][tid];
+            a.out[i0 + tid] = o;
+        }
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------------ host side
+
+bool moe_packed_planes(const void* W, int type, int K, size_t row_bytes, const uint8_t** v, const uint8_t** s);
+void moe_mv_shape(int type, int K, int* lanes, int* units_per_lane);
+
+namespace {
+
+template <int TYPE, int NI, int LO, int NO>
+hipError_t launch_fused(const FArgs& a, int nblocks, hipStream_t st) {
+    return launch_kernel(k_fused_decode<TYPE, NI, LO, NO>, dim3(nblocks), dim3(256), 0, st, a);
+}
+
+// Gate / up: 64 lanes per row, NI units per lane (K = E = 2048 or 4096). Down: the per-operation kernel's
+// (lanes, units) for K = FE: 512 -> (16, 1), 768 -> (8, 3), 1024 -> (32, 1), 1536 -> (16, 3), 2048 -> (64, 1).
+template <int TYPE>
+hipError_t launch_fused_t(const FArgs& a, int ni, int lo, int no, int nblocks, hipStream_t st) {
+#define FD_CASE(I, L, O) \
+    if (ni == I && lo == L && no == O) return launch_fused<TYPE, I, L, O>(a, nblocks, st);
+    FD_CASE(1, 16, 1) FD_CASE(1, 8, 3) FD_CASE(1, 32, 1) FD_CASE(1, 16, 3) FD_CASE(1, 64, 1)
+    FD_CASE(2, 16, 1) FD_CASE(2, 8, 3) FD_CASE(2, 32, 1) FD_CASE(2, 16, 3) FD_CASE(2, 64, 1)
+#undef FD_CASE
+    return hipErrorInvalidDeviceFunction;
+}
+
+bool fused_shape_ok(int ni, int lo, int no) {
+    if (ni != 1 && ni != 2) return false;
+    return (lo == 16 && no == 1) || (lo == 8 && no == 3) || (lo == 32 && no == 1) || (lo == 16 && no == 3) ||
+           (lo == 64 && no == 1);
+}
+
+int cu_count() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n = 0;
+    }
+    return n;
+}
+
+}  // namespace
+
+// Scratch bytes of the fused kernel: barrier words, logits, gate, the quantized down input
+size_t moe_fused_scratch_bytes(const moe_layer_desc* d) {
+    const int NS = d->n_used + (d->s_gate ? 1 : 0);
+    auto a256 = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    return a256(16) + a256((size_t)d->n_expert * 4) + a256(4) + a256((size_t)NS * d->n_ff) +
+           a256((size_t)NS * d->n_ff / 32 * 4);
+}
+
+// Whether the fused kernel takes this layer at T = 1: a Q8_0-activation type, every expert matrix registered in
+// split-plane form, and shapes the instantiations cover. Fills the kernel arguments.
+bool moe_fused_prepare(const moe_layer_desc* d, FArgs& a) {
+    const int type = d->type, E = d->n_embd, FE = d->n_ff, NU = d->n_used;
+    if (type != QT_Q8_0 && type != QT_ROCMFP4 && type != QT_ROCMFP4_FAST) return false;
+    if (E % 2048 || E > FD_MAX_E || FE % 256 || NU > 64 || d->n_expert > ROUTER_MAX_E) return false;
+    int li, ni, lo, no;
+    moe_mv_shape(type, E, &li, &ni);
+    moe_mv_shape(type, FE, &lo, &no);
+    if (li != 64 || !fused_shape_ok(ni, lo, no)) return false;
+    const int NS = NU + (d->s_gate ? 1 : 0);
+    if (NS > 16 || cu_count() == 0) return false;
+    const size_t rb_in = (size_t)E / 32 * (type == QT_Q8_0 ? 34 : type == QT_ROCMFP4 ? 18 : 17);
+    const size_t rb_out = (size_t)FE / 32 * (type == QT_Q8_0 ? 34 : type == QT_ROCMFP4 ? 18 : 17);
+    const void* W[6] = {d->w_gate, d->w_up, d->w_down, d->s_gate, d->s_up, d->s_down};
+    for (int i = 0; i < 6; ++i) {
+        a.v[i] = a.s[i] = nullptr;
+        if (!W[i]) {
+            if (i < 3 || d->s_gate) return false;
+            continue;
+        }
+        if (!moe_packed_planes(W[i], type, i % 3 == 2 ? FE : E, i % 3 == 2 ? rb_out : rb_in, &a.v[i], &a.s[i]))
+            return false;
+    }
+    a.vrb_in = type == QT_Q8_0 ? E : E / 2;
+    a.srb_in = type == QT_ROCMFP4_FAST ? E / 32 : E / 16;
+    a.vrb_out = type == QT_Q8_0 ? FE : FE / 2;
+    a.srb_out = type == QT_ROCMFP4_FAST ? FE / 32 : FE / 16;
+    a.E = E;
+    a.NE = d->n_expert;
+    a.NU = NU;
+    a.FE = FE;
+    a.NS = NS;
+    a.w_router = d->w_router;
+    a.w_shexp = d->w_shexp;
+    a.has_gate = d->s_gate && d->w_shexp ? 1 : 0;
+    return true;
+}
+
+hipError_t moe_fused_launch(const moe_layer_desc* d, FArgs& a, void* scratch, hipStream_t st) {
+    auto a256 = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    char* p = (char*)scratch;
+    a.bar = (unsigned*)p;
+    p += a256(16);
+    a.logits = (float*)p;
+    p += a256((size_t)a.NE * 4);
+    a.sg = (float*)p;
+    p += a256(4);
+    a.act_q = (int8_t*)p;
+    p += a256((size_t)a.NS * a.FE);
+    a.act_d = (float*)p;
+    int li, ni, lo, no;
+    moe_mv_shape(d->type, a.E, &li, &ni);
+    moe_mv_shape(d->type, a.FE, &lo, &no);
+    const int nblocks = cu_count();
+    switch (d->type) {
+    case QT_Q8_0: return launch_fused_t<QT_Q8_0>(a, ni, lo, no, nblocks, st);
+    case QT_ROCMFP4: return launch_fused_t<QT_ROCMFP4>(a, ni, lo, no, nblocks, st);
+    default: return launch_fused_t<QT_ROCMFP4_FAST>(a, ni, lo, no, nblocks, st);
+    }
+}
+
+bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits, float* out, int* ids_out,
+                   float* wts_out, void* scratch, hipStream_t st, hipError_t* err) {
+    FArgs a = {};
+    if (!moe_fused_prepare(d, a)) return false;
+    a.x = x;
+    a.logits_in = logits;
+    a.out = out;
+    a.ids_out = ids_out;
+    a.wts_out = wts_out;
+    *err = moe_fused_launch(d, a, scratch, st);
+    return true;
+}

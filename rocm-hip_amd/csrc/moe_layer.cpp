@@ -5,8 +5,19 @@
 
 #include <stdint.h>
 
+#include <atomic>
+
 #include "gpu_ops.h"
 #include "qmatvec.h"
+
+struct FArgs;
+size_t moe_fused_scratch_bytes(const moe_layer_desc* d);
+
+// The fused decode kernel's arguments are built in fused_decode.hip; this file only sees these entry points
+bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits, float* out, int* ids_out,
+                   float* wts_out, void* scratch, hipStream_t st, hipError_t* err);
+
+static std::atomic<int> g_fused{1};
 
 namespace {
 
@@ -25,7 +36,8 @@ size_t row_size(int type, int k) {
 
 // Scratch carve-up; every piece 256-byte aligned
 struct Plan {
-    size_t logits, ids, wts, sg, qx, g, u, act, qa, down, sg_, su, sact, qs, sout, tok, pair, ntile, te, ts, tn, total;
+    size_t fused, logits, ids, wts, sg, qx, g, u, act, qa, down, sg_, su, sact, qs, sout, tok, pair, ntile, te, ts, tn,
+        total;
     int NS, qx_k, qa_k, qs_k, max_tiles, tile;
 };
 
@@ -35,11 +47,12 @@ Plan plan(const moe_layer_desc* d, int T) {
     const bool sh = d->s_gate != nullptr;
     p.NS = NU + (sh ? 1 : 0);
     p.tile = 64;
+    p.fused = moe_fused_scratch_bytes(d);
     p.max_tiles = gpu_moe_max_tiles(T, NU, NE, p.tile);
     p.qx_k = r256((long long)T * E);
     p.qa_k = r256((long long)T * p.NS * FE);
     p.qs_k = r256((long long)T * FE);
-    size_t o = 0;
+    size_t o = a256(p.fused);  // the fused kernel's region first: its barrier words open the scratch
     auto take = [&](size_t bytes) {
         const size_t at = o;
         o += a256(bytes);
@@ -78,6 +91,14 @@ Plan plan(const moe_layer_desc* d, int T) {
 
 }  // namespace
 
+extern "C" void moe_layer_set_fused(int enable) { g_fused.store(enable ? 1 : 0); }
+
+extern "C" int moe_layer_fused_error(const void* scratch) {
+    unsigned w[3] = {0, 0, 0};
+    if (!scratch || hipMemcpy(w, scratch, sizeof(w), hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    return (int)w[2];
+}
+
 extern "C" size_t moe_layer_scratch_bytes(const moe_layer_desc* d, int max_t) {
     if (!d || max_t <= 0) return 0;
     return plan(d, max_t).total;
@@ -91,6 +112,10 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
     if (scratch_bytes < p.total) return hipErrorInvalidValue;
     const int E = d->n_embd, NE = d->n_expert, NU = d->n_used, FE = d->n_ff, type = d->type;
     const bool sh = d->s_gate != nullptr;
+    if (T == 1 && g_fused.load(std::memory_order_relaxed)) {
+        hipError_t e = hipSuccess;
+        if (moe_fused_try(d, x, logits_in, out, ids_out, wts_out, scratch, st, &e)) return e;
+    }
     const size_t rb_in = row_size(type, E), rb_out = row_size(type, FE);
     char* s = (char*)scratch;
     float* lg = (float*)(s + p.logits);

@@ -10,6 +10,7 @@
 #include "moe_common.h"
 #include "q8_quant.h"
 #include "qmatvec.h"
+#include "router_dev.h"
 
 static Q8Out q8_out(const qmatvec_q8* q) {
     Q8Out o = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0};
@@ -130,41 +131,14 @@ __global__ void __launch_bounds__(256) k_add_rmsnorm(const float* x_in, const fl
 
 // ------------------------------------------------------------------ router logits: F32 matvec
 
-// Decode: one 256-thread workgroup per row, 16-byte loads all issued up front (K / 1024 per thread), x
-// re-read from L1 / L2. y[row] = W[row] . x
-__device__ __forceinline__ float block256_sum(float v, float* part) {
-    v = wave_sum(v);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
-    __syncthreads();
-    const float s = (part[0] + part[1]) + (part[2] + part[3]);
-    __syncthreads();
-    return s;
-}
-
+// Decode: one 256-thread workgroup per row and token, 16-byte loads (K / 1024 per thread), x re-read from L1 /
+// L2. y[row] = W[row] . x
 __global__ void __launch_bounds__(256) k_matvec_f32(const float* W, long long ldw, const float* x, float* y, int N,
                                                    int K) {
     __shared__ float part[4];
-    const int row = blockIdx.x, tid = threadIdx.x;
-    const float* wr = W + (size_t)row * ldw;
-    x += (size_t)blockIdx.y * K;  // token
-    y += (size_t)blockIdx.y * N;
-    float acc = 0.0f;
-    if ((K & 3) == 0 && (((uintptr_t)wr | (uintptr_t)x) & 15) == 0) {
-        const float4* w4 = (const float4*)wr;
-        const float4* x4 = (const float4*)x;
-#pragma unroll 4
-        for (int i = tid; i < K / 4; i += 256) {
-            const float4 a = w4[i], b = x4[i];
-            acc = fmaf(a.x, b.x, acc);
-            acc = fmaf(a.y, b.y, acc);
-            acc = fmaf(a.z, b.z, acc);
-            acc = fmaf(a.w, b.w, acc);
-        }
-    } else {
-        for (int i = tid; i < K; i += 256) acc = fmaf(wr[i], x[i], acc);
-    }
-    acc = block256_sum(acc, part);
-    if (tid == 0) y[row] = acc;
+    const int row = blockIdx.x;
+    const float acc = f32_row_dot(W + (size_t)row * ldw, x + (size_t)blockIdx.y * K, K, part);
+    if (threadIdx.x == 0) y[(size_t)blockIdx.y * N + row] = acc;
 }
 
 // Prefill: tiles of 32 tokens x 32 rows (enough workgroups to fill the chip at a few thousand tokens), K staged
@@ -206,73 +180,20 @@ __global__ void __launch_bounds__(256) k_matmul_f32(const float* W, long long ld
 
 // ------------------------------------------------------------------ router (src/gpu_ops.hip:185-241)
 
-// One 256-thread workgroup per token. The logits go to LDS; softmax max and sum by DPP wave reductions. The
-// selection ranks every expert by counting the experts that beat it (a larger logit, or an equal one at a lower
-// index): softmax is strictly monotonic, so this is the order of the probabilities, ties to the lower index,
-// and the experts of rank < n_used are the selection in descending order. Every count reads the same LDS
-// address across the wave (a broadcast), with no cross-lane dependency chain. The selected probabilities
-// exp(l - max) / sum are renormalised by max(their sum, 6.103515625e-5), summed in rank order.
-#define ROUTER_MAX_E 1024
+// One 256-thread workgroup per token: the shared-expert gate, then router_select (router_dev.h).
 __global__ void __launch_bounds__(256) k_router(const float* logits, const float* x, const float* w_shexp, int* ids,
                                                 float* wts, float* sg, int ne, int nu, int n, int ids_stride) {
     __shared__ __attribute__((aligned(16))) float sl[ROUTER_MAX_E];
     __shared__ float part[4];
     __shared__ float sel_p[64];
     const int t = blockIdx.x, tid = threadIdx.x;
-    const float* lg = logits + (size_t)t * ne;
-    for (int e = tid; e < ne; e += 256) sl[e] = lg[e];
-    const int ne4 = (ne + 3) & ~3;
-    for (int e = ne + tid; e < ne4; e += 256) sl[e] = -INFINITY;  // pad: never beats a real expert
-
-    if (w_shexp) {  // the shared-expert gate (uniform branch)
-        const float* xr = x + (size_t)t * n;
-        float d = 0.0f;
-        if ((n & 3) == 0 && (((uintptr_t)xr | (uintptr_t)w_shexp) & 15) == 0) {
-            for (int i = tid; i < n / 4; i += 256) {
-                const float4 a = ((const float4*)xr)[i], b = ((const float4*)w_shexp)[i];
-                d += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
-            }
-        } else {
-            for (int i = tid; i < n; i += 256) d += xr[i] * w_shexp[i];
-        }
-        d = block256_sum(d, part);
-        if (tid == 0) sg[t] = 1.0f / (1.0f + expf(-d));
+    if (w_shexp) {  // (uniform branch)
+        const float g = shexp_gate(x + (size_t)t * n, w_shexp, n, part);
+        if (tid == 0) sg[t] = g;
     }
-
-    float mx = -INFINITY;
-    for (int e = tid; e < ne; e += 256) mx = fmaxf(mx, lg[e]);
-    mx = wave_max(mx);
-    if ((tid & 63) == 0) part[tid >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
-    __syncthreads();
-    float sum = 0.0f;
-    for (int e = tid; e < ne; e += 256) sum += expf(sl[e] - mx);
-    sum = block256_sum(sum, part);
-    const float inv = 1.0f / sum;
-
     int* id_row = ids + (size_t)t * ids_stride;
-    for (int e = tid; e < ne; e += 256) {  // uniform trip count per wave except the last
-        const float v = sl[e];
-        int rank = 0;
-        for (int k = 0; k < ne4; k += 4) {
-            const float4 c = *(const float4*)(sl + k);
-            rank += (c.x > v || (c.x == v && k < e)) + (c.y > v || (c.y == v && k + 1 < e)) +
-                    (c.z > v || (c.z == v && k + 2 < e)) + (c.w > v || (c.w == v && k + 3 < e));
-        }
-        if (rank < nu) {
-            id_row[rank] = e;
-            sel_p[rank] = expf(v - mx) * inv;
-        }
-    }
+    router_select(logits + (size_t)t * ne, ne, nu, sl, part, sel_p, id_row, wts + (size_t)t * nu);
     if (tid == 0 && ids_stride > nu) id_row[nu] = -1;
-    __syncthreads();
-    if (tid == 0) {
-        float ws = 0.0f;
-        for (int r = 0; r < nu; ++r) ws += sel_p[r];
-        ws = fmaxf(ws, 6.103515625e-5f);
-        for (int r = 0; r < nu; ++r) wts[(size_t)t * nu + r] = sel_p[r] / ws;
-    }
 }
 
 // ------------------------------------------------------------------ C ABI

@@ -41,7 +41,7 @@ def main():
 
     lay = {}
     for t in TYPES:
-        E, FE = (256, 256) if t == 12 else (256, 64)
+        E, FE = (256, 256) if t == 12 else (256, 128)
         spec = synth.LayerSpec(t, E, 3, 2, FE, shared=(t != 12))
         L = synth.make_layer(spec, seed=100 + t)
         xx = np.random.default_rng(200 + t).standard_normal((3, E)).astype(np.float32)
