@@ -7,10 +7,9 @@
 //           experts' width and type), SwiGLU quantized for down, down, moe_combine;
 //   T 2..7: the same per token (each token's experts read once per token);
 //   T >= 8: gpu_moe_group, the grouped gate / up / down on the expert tiles, the shared expert dense, combine.
-// T == 1 with every expert matrix registered (qmatvec_pack_weights) runs as one persistent kernel with the same
-// results bit for bit. All buffers are device memory; scratch is caller-owned (moe_layer_scratch_bytes) and
-// must be zero-filled once before its first use (it opens with the fused kernel's barrier words, which every
-// completed call leaves at zero). Asynchronous on `stream`.
+// T == 1 with every expert matrix registered (qmatvec_pack_weights) runs as three fused kernels with the same
+// results bit for bit. All buffers are device memory; scratch is caller-owned (moe_layer_scratch_bytes).
+// Asynchronous on `stream`.
 
 #ifndef MOE_LAYER_H
 #define MOE_LAYER_H
@@ -46,13 +45,15 @@ size_t moe_layer_scratch_bytes(const moe_layer_desc* d, int max_t);
 hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x, const float* logits, int T, float* out,
                              int* ids_out, float* wts_out, void* scratch, size_t scratch_bytes, hipStream_t stream);
 
-// No counterpart in the reference. Whether T == 1 calls may use the fused kernel (1, the default) or always take
+// No counterpart in the reference. Whether T == 1 calls may use the fused kernels (1, the default) or always take
 // the per-operation launches (0); process-wide.
 void moe_layer_set_fused(int enable);
 
-// No counterpart in the reference. The fused kernel's error word in scratch (synchronous read): non-zero after a
-// grid barrier gave up (the grid was not co-resident); the scratch must then be zero-filled again.
-int moe_layer_fused_error(const void* scratch);
+// No counterpart in the reference (its QWEN_PROFILE times sections on the host). Profiling: every later fused
+// layer writes wall-clock stamps (100 MHz) per workgroup to stamps: [workgroup][6], kernel 1 in column 0,
+// kernel 2 in 1..3 (start, routed, done), kernel 3 in 4, 5; rows for the largest grid (max(NE + 1, NS * FE / 32,
+// E / 8)); NULL stops.
+void moe_layer_fused_stamps(void* stamps);
 
 #ifdef __cplusplus
 }

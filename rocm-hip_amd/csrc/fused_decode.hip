@@ -1,21 +1,18 @@
-// fused_decode.hip -- one batch-1 MoE FFN layer in one persistent kernel (gfx950, wave64).
+// fused_decode.hip -- one batch-1 MoE FFN layer in three kernels (gfx950, wave64).
 //
-// The multi-kernel layer (router logits, router, quantize, gate/up, SwiGLU, down, combine) costs seven launches,
+// The per-operation layer (router logits, router, quantize, gate/up, SwiGLU, down, combine) costs seven launches,
 // each with ~2.5 us of ramp and tail on MI355X, while the layer's ~25-40 MB of weights take 3-5 us at HBM speed.
-// Here one grid of one workgroup per CU runs the layer in three phases separated by two grid barriers:
-//   A  every workgroup quantizes x into LDS (the activation quantizer's exact expressions); the router-logit
-//      rows are spread over the workgroups; one workgroup computes the shared-expert gate;
-//   B  every workgroup routes (the router's own code on the logits), then works through units of (slot, 32-row
-//      block of FE): the 32 gate rows and 32 up rows of the slot's expert, SwiGLU, and the Q8_0 quantization of
-//      those 32 values, which are one Q8_0 block of the down projection's input;
-//   C  units of 8 output rows: their down rows for every slot, then the combine in slot order.
+// Here the layer is three launches with no grid-wide synchronisation inside any of them:
+//   1  one workgroup per router-logit row, plus one that quantizes x (the activation quantizer's expressions)
+//      and computes the shared-expert gate;
+//   2  one workgroup per (slot, 32-row block of FE): it routes (the router's own code on the logits, every
+//      workgroup for itself; workgroup 0 also publishes ids / weights), then computes the slot expert's 32 gate
+//      and 32 up rows, SwiGLU, and the Q8_0 quantization of those 32 values (one Q8_0 block of down's input);
+//   3  one workgroup per 8 output rows: their down rows for every slot, then the combine in slot order.
 // Every sum is formed in the same order as the per-operation kernels (rows_dot's lane groups and DPP group sums,
-// the same router, quantizer and combine), so the layer's output equals moe_layer_forward's multi-kernel path
-// bit for bit.
-//
-// The barriers spin on a generation word with a bounded wait: a barrier that does not complete (the grid not
-// co-resident) sets an error word and the kernel exits instead of hanging. The barrier words live in the
-// caller's scratch, zero before the first launch and zero again after every completed launch.
+// the same router, quantizer and combine), so the layer's output equals the per-operation path bit for bit.
+// (A single persistent kernel with two grid barriers was measured slower: each barrier's cross-XCD fences and
+// 256-way atomic arrival cost ~10 us on MI355X, more than a kernel boundary.)
 
 #include "expert_units.h"
 #include "host_common.h"
@@ -25,7 +22,6 @@
 
 #define FD_MAX_E 4096
 #define FD_RB 8                 // output rows per down unit
-#define FD_SPIN_LIMIT (1u << 21)  // ~0.1 s of polling before a barrier gives up
 
 struct FArgs {
     const float* x;          // [E]
@@ -40,40 +36,20 @@ struct FArgs {
     float* wts_out;          // [NU] or nullptr
     float* logits;           // scratch [NE]
     float* sg;               // scratch [1]
+    int8_t* xq;              // scratch: x quantized, Q8_0 values [E] and scales [E / 32]
+    float* xd;
+    int* ids;                // scratch: the routing [NU]
+    float* wts;
     int8_t* act_q;           // scratch [NS][FE]
     float* act_d;            // scratch [NS][FE / 32]
-    unsigned* bar;           // scratch: count, generation, error
+    unsigned long long* stamps;  // optional timestamps (profiling): [kernel 1 | 2 | 3 workgroups][6], nullptr: none
     int E, NE, NU, FE, NS, has_gate;
 };
 
-// Grid barrier: the last arriving workgroup resets the count and bumps the generation. Agent-scope atomics and
-// fences make the phase's global writes visible across XCDs. Returns false after a timeout.
-__device__ __forceinline__ bool grid_sync(unsigned* bar, unsigned nblocks, int* flag) {
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned g0 = __hip_atomic_load(&bar[1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-        __threadfence();
-        const unsigned arrived = __hip_atomic_fetch_add(&bar[0], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        int ok = 1;
-        if (arrived == nblocks - 1) {
-            __hip_atomic_store(&bar[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_fetch_add(&bar[1], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            unsigned spins = 0;
-            while (__hip_atomic_load(&bar[1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == g0) {
-                __builtin_amdgcn_s_sleep(2);
-                if (++spins > FD_SPIN_LIMIT) {
-                    __hip_atomic_fetch_or(&bar[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    ok = 0;
-                    break;
-                }
-            }
-        }
-        __threadfence();
-        *flag = ok;
-    }
-    __syncthreads();
-    return *flag != 0;
+// Timestamp k of this workgroup (the 100 MHz wall clock), when stamps are requested: kernel 1 uses slots 0,
+// kernel 2 slots 1..3, kernel 3 slots 4, 5 of row blockIdx.x of a [max grid][6] table
+__device__ __forceinline__ void stamp(const FArgs& a, int k) {
+    if (a.stamps && threadIdx.x == 0) a.stamps[blockIdx.x * 6 + k] = wall_clock64();
 }
 
 // The down phase's row dots: R row dots per lane group of L lanes, each with its own weight row and input row;
@@ -101,23 +77,17 @@ __device__ __forceinline__ void rows_dot_multi(const uint8_t* const vr[R], const
     }
 }
 
-template <int TYPE, int NUPL_IN, int L_OUT, int NUPL_OUT>
-__global__ void __launch_bounds__(256) k_fused_decode(FArgs a) {
-    __shared__ __attribute__((aligned(16))) int8_t sxq[FD_MAX_E];
-    __shared__ __attribute__((aligned(16))) float sxd[FD_MAX_E / 32];
-    __shared__ __attribute__((aligned(16))) float sl[ROUTER_MAX_E];
+// ---- kernel 1: router logits (workgroups 0 .. NE - 1), x quantized + the shared gate (workgroup NE)
+__global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
     __shared__ float part[4];
-    __shared__ float sel_p[64];
-    __shared__ int s_ids[65];
-    __shared__ float s_wts[64];
-    __shared__ float gu[2][32];
-    __shared__ float downv[16][FD_RB];
-    __shared__ int flag;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const unsigned nb = gridDim.x;
-    const int E = a.E, FE = a.FE, NU = a.NU, NS = a.NS;
-
-    // ---- phase A: x quantized into LDS (Q8_0 per 32 values: 4 threads of 8 values), router logits, gate
+    const int tid = threadIdx.x, E = a.E;
+    stamp(a, 0);
+    if ((int)blockIdx.x < a.NE) {
+        const float y = f32_row_dot(a.w_router + (size_t)blockIdx.x * E, a.x, E, part);
+        if (tid == 0) a.logits[blockIdx.x] = y;
+        return;
+    }
+    // Q8_0 per 32 values (4 threads of 8 values): the quantizer's expressions
     for (int base = 0; base < E; base += 2048) {
         const int i0 = base + 8 * tid;
         float v[8];
@@ -130,105 +100,124 @@ __global__ void __launch_bounds__(256) k_fused_decode(FArgs a) {
         am = group_max<4>(am);
         const float id = am != 0.0f ? 127.0f / am : 0.0f;
         if (i0 < E) {
+            int q[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) sxq[i0 + j] = (int8_t)(int)rintf(v[j] * id);
-            if ((tid & 3) == 0) sxd[i0 / 32] = __half2float(__float2half(am / 127.0f));
+            for (int j = 0; j < 8; ++j) q[j] = (int)rintf(v[j] * id);
+            *(uint2*)(a.xq + i0) = make_uint2((q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) |
+                                                  ((uint32_t)q[3] << 24),
+                                              (q[4] & 0xff) | ((q[5] & 0xff) << 8) | ((q[6] & 0xff) << 16) |
+                                                  ((uint32_t)q[7] << 24));
+            if ((tid & 3) == 0) a.xd[i0 / 32] = __half2float(__float2half(am / 127.0f));
         }
     }
-    if (!a.logits_in)
-        for (int r = blockIdx.x; r < a.NE; r += nb) {
-            const float y = f32_row_dot(a.w_router + (size_t)r * E, a.x, E, part);
-            if (tid == 0) a.logits[r] = y;
-        }
-    if (a.has_gate && blockIdx.x == nb - 1) {
+    if (a.has_gate) {
         const float g = shexp_gate(a.x, a.w_shexp, E, part);
         if (tid == 0) a.sg[0] = g;
     }
-    if (!grid_sync(a.bar, nb, &flag)) return;
+}
 
-    // ---- phase B: routing, then gate / up / SwiGLU / quantize per (slot, 32-row block)
+// ---- kernel 2: routing, then gate / up / SwiGLU / quantize of unit (slot, 32-row block)
+template <int TYPE, int NUPL_IN>
+__global__ void __launch_bounds__(256) k_fd_gate_up(FArgs a) {
+    __shared__ __attribute__((aligned(16))) float sl[ROUTER_MAX_E];
+    __shared__ float part[4];
+    __shared__ float sel_p[64];
+    __shared__ int s_ids[65];
+    __shared__ float s_wts[64];
+    __shared__ float gu[2][32];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int FE = a.FE, NU = a.NU, nbf = FE / 32;
+    const int slot = blockIdx.x / nbf, b = blockIdx.x - slot * nbf;
+    stamp(a, 1);
     router_select(a.logits_in ? a.logits_in : a.logits, a.NE, NU, sl, part, sel_p, s_ids, s_wts);
-    if (tid == 0) s_ids[NU] = -1;  // the shared expert's slot
-    __syncthreads();
-    if (blockIdx.x == 0 && tid < NU) {
+    if (blockIdx.x == 0 && tid < NU) {  // the routing for kernel 3 and the caller
+        a.ids[tid] = s_ids[tid];
+        a.wts[tid] = s_wts[tid];
         if (a.ids_out) a.ids_out[tid] = s_ids[tid];
         if (a.wts_out) a.wts_out[tid] = s_wts[tid];
     }
-    const int nbf = FE / 32;
-    for (int u = blockIdx.x; u < NS * nbf; u += nb) {
-        const int slot = u / nbf, b = u - slot * nbf;
-        const int e = s_ids[slot];
-        const int mat = w >> 1;  // waves 0, 1: gate rows; 2, 3: up rows
-        const int mi = e >= 0 ? mat : 3 + mat;
-        const long long rbase = e >= 0 ? (long long)e * FE : 0;
-        const uint8_t* vb = a.v[mi] + rbase * a.vrb_in;
-        const uint8_t* sb = a.s[mi] + rbase * a.srb_in;
-        float acc[16];
-        rows_dot<TYPE, true, 64, 16, NUPL_IN>(vb, sb, a.vrb_in, a.srb_in, 32 * b + 16 * (w & 1), 1, FE, sxq, sxd,
-                                              nullptr, E, lane, acc);
-        if (lane == 0)
+    stamp(a, 2);
+    const int e = slot < NU ? s_ids[slot] : -1;
+    const int mat = w >> 1;  // waves 0, 1: gate rows; 2, 3: up rows
+    const int mi = e >= 0 ? mat : 3 + mat;
+    const long long rbase = e >= 0 ? (long long)e * FE : 0;
+    const uint8_t* vb = a.v[mi] + rbase * a.vrb_in;
+    const uint8_t* sb = a.s[mi] + rbase * a.srb_in;
+    float acc[16];
+    rows_dot<TYPE, true, 64, 16, NUPL_IN>(vb, sb, a.vrb_in, a.srb_in, 32 * b + 16 * (w & 1), 1, FE, a.xq, a.xd,
+                                          nullptr, a.E, lane, acc);
+    if (lane == 0)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) gu[mat][16 * (w & 1) + r] = acc[r];
-        __syncthreads();
-        if (w == 0) {  // SwiGLU (the swiglu kernel's expression) and the Q8_0 block of these 32 values
-            const int t = lane & 31;
-            const float g = gu[0][t], uu = gu[1][t];
-            const float act = g / (1.0f + __expf(-g)) * uu;
-            const float am = group_max<32>(fabsf(act));
-            const float id = am != 0.0f ? 127.0f / am : 0.0f;
-            if (lane < 32) {
-                a.act_q[(long long)slot * FE + 32 * b + t] = (int8_t)(int)rintf(act * id);
-                if (t == 0) a.act_d[(long long)slot * nbf + b] = __half2float(__float2half(am / 127.0f));
-            }
+        for (int r = 0; r < 16; ++r) gu[mat][16 * (w & 1) + r] = acc[r];
+    __syncthreads();
+    if (w == 0) {  // SwiGLU (the swiglu kernel's expression) and the Q8_0 block of these 32 values
+        const int t = lane & 31;
+        const float g = gu[0][t], uu = gu[1][t];
+        const float act = g / (1.0f + __expf(-g)) * uu;
+        const float am = group_max<32>(fabsf(act));
+        const float id = am != 0.0f ? 127.0f / am : 0.0f;
+        if (lane < 32) {
+            a.act_q[(long long)slot * FE + 32 * b + t] = (int8_t)(int)rintf(act * id);
+            if (t == 0) a.act_d[(long long)slot * nbf + b] = __half2float(__float2half(am / 127.0f));
         }
-        __syncthreads();
     }
-    if (!grid_sync(a.bar, nb, &flag)) return;
+    stamp(a, 3);
+}
 
-    // ---- phase C: down rows of every slot for FD_RB output rows, then the combine in slot order. Lane groups of
-    // L_OUT lanes with NUPL_OUT units each: the per-operation down kernel's shape for this K, so the same sums.
-    const float sgv = a.has_gate ? a.sg[0] : 1.0f;
+// ---- kernel 3: down rows of every slot for FD_RB output rows, then the combine in slot order. Lane groups of
+// L_OUT lanes with NUPL_OUT units each: the per-operation down kernel's shape for this K, so the same sums.
+template <int TYPE, int L_OUT, int NUPL_OUT>
+__global__ void __launch_bounds__(256) k_fd_down(FArgs a) {
+    __shared__ int s_ids[65];
+    __shared__ float s_wts[64];
+    __shared__ float downv[16][FD_RB];
+    const int tid = threadIdx.x, E = a.E, FE = a.FE, NU = a.NU, NS = a.NS;
+    stamp(a, 4);
+    if (tid < NU) {
+        s_ids[tid] = a.ids[tid];
+        s_wts[tid] = a.wts[tid];
+    }
+    if (tid == 0) s_ids[NU] = -1;  // the shared expert's slot
+    __syncthreads();
     constexpr int NG = 256 / L_OUT;  // lane groups per workgroup
     constexpr int RR = 4;            // row dots per group and round
     const int gl = tid & (L_OUT - 1), grp = tid / L_OUT;
     const int ndots = NS * FD_RB;
-    for (int t = blockIdx.x; t < E / FD_RB; t += nb) {
-        const int i0 = t * FD_RB;
-        for (int k0 = 0; k0 < ndots; k0 += NG * RR) {
-            const uint8_t* vr[RR];
-            const uint8_t* sr[RR];
-            const int8_t* xq[RR];
-            const float* xd[RR];
+    const int i0 = blockIdx.x * FD_RB;
+    for (int k0 = 0; k0 < ndots; k0 += NG * RR) {
+        const uint8_t* vr[RR];
+        const uint8_t* sr[RR];
+        const int8_t* xq[RR];
+        const float* xd[RR];
+#pragma unroll
+        for (int r = 0; r < RR; ++r) {
+            const int k = min(k0 + grp + NG * r, ndots - 1);  // idle row dots repeat the last one (not stored)
+            const int slot = k / FD_RB, i = k - slot * FD_RB;
+            const int e = s_ids[slot];
+            const long long row = e >= 0 ? (long long)e * E + i0 + i : i0 + i;
+            const int mi = e >= 0 ? 2 : 5;
+            vr[r] = a.v[mi] + row * a.vrb_out;
+            sr[r] = a.s[mi] + row * a.srb_out;
+            xq[r] = a.act_q + (long long)slot * FE;
+            xd[r] = a.act_d + (long long)slot * (FE / 32);
+        }
+        float acc[RR];
+        rows_dot_multi<TYPE, L_OUT, RR, NUPL_OUT>(vr, sr, xq, xd, FE / 32, gl, acc);
+        if (gl == 0)
 #pragma unroll
             for (int r = 0; r < RR; ++r) {
-                const int k = min(k0 + grp + NG * r, ndots - 1);  // idle row dots repeat the last one (not stored)
-                const int slot = k / FD_RB, i = k - slot * FD_RB;
-                const int e = s_ids[slot];
-                const long long row = e >= 0 ? (long long)e * E + i0 + i : i0 + i;
-                const int mi = e >= 0 ? 2 : 5;
-                vr[r] = a.v[mi] + row * a.vrb_out;
-                sr[r] = a.s[mi] + row * a.srb_out;
-                xq[r] = a.act_q + (long long)slot * FE;
-                xd[r] = a.act_d + (long long)slot * (FE / 32);
+                const int k = k0 + grp + NG * r;
+                if (k < ndots) downv[k / FD_RB][k % FD_RB] = acc[r];
             }
-            float acc[RR];
-            rows_dot_multi<TYPE, L_OUT, RR, NUPL_OUT>(vr, sr, xq, xd, FE / 32, gl, acc);
-            if (gl == 0)
-#pragma unroll
-                for (int r = 0; r < RR; ++r) {
-                    const int k = k0 + grp + NG * r;
-                    if (k < ndots) downv[k / FD_RB][k % FD_RB] = acc[r];
-                }
-        }
-        __syncthreads();
-        if (tid < FD_RB) {  // the combine kernel's expression
-            float o = s_wts[0] * downv[0][tid];
-            for (int j = 1; j < NU; ++j) o += s_wts[j] * downv[j][tid];
-            if (NS > NU) o += a.has_gate ? downv[NU][tid] * sgv : downv[NU][tid];
-            a.out[i0 + tid] = o;
-        }
-        __syncthreads();
     }
+    __syncthreads();
+    if (tid < FD_RB) {  // the combine kernel's expression
+        float o = s_wts[0] * downv[0][tid];
+        for (int j = 1; j < NU; ++j) o += s_wts[j] * downv[j][tid];
+        if (NS > NU) o += a.has_gate ? downv[NU][tid] * a.sg[0] : downv[NU][tid];
+        a.out[i0 + tid] = o;
+    }
+    stamp(a, 5);
 }
 
 // ------------------------------------------------------------------ host side
@@ -239,16 +228,20 @@ void moe_mv_shape(int type, int K, int* lanes, int* units_per_lane);
 namespace {
 
 template <int TYPE, int NI, int LO, int NO>
-hipError_t launch_fused(const FArgs& a, int nblocks, hipStream_t st) {
-    return launch_kernel(k_fused_decode<TYPE, NI, LO, NO>, dim3(nblocks), dim3(256), 0, st, a);
+hipError_t launch_fused(const FArgs& a, hipStream_t st) {
+    hipError_t e = launch_kernel(k_fd_logits, dim3(a.NE + 1), dim3(256), 0, st, a);
+    if (e == hipSuccess)
+        e = launch_kernel(k_fd_gate_up<TYPE, NI>, dim3(a.NS * (a.FE / 32)), dim3(256), 0, st, a);
+    if (e == hipSuccess) e = launch_kernel(k_fd_down<TYPE, LO, NO>, dim3(a.E / FD_RB), dim3(256), 0, st, a);
+    return e;
 }
 
 // Gate / up: 64 lanes per row, NI units per lane (K = E = 2048 or 4096). Down: the per-operation kernel's
 // (lanes, units) for K = FE: 512 -> (16, 1), 768 -> (8, 3), 1024 -> (32, 1), 1536 -> (16, 3), 2048 -> (64, 1).
 template <int TYPE>
-hipError_t launch_fused_t(const FArgs& a, int ni, int lo, int no, int nblocks, hipStream_t st) {
+hipError_t launch_fused_t(const FArgs& a, int ni, int lo, int no, hipStream_t st) {
 #define FD_CASE(I, L, O) \
-    if (ni == I && lo == L && no == O) return launch_fused<TYPE, I, L, O>(a, nblocks, st);
+    if (ni == I && lo == L && no == O) return launch_fused<TYPE, I, L, O>(a, st);
     FD_CASE(1, 16, 1) FD_CASE(1, 8, 3) FD_CASE(1, 32, 1) FD_CASE(1, 16, 3) FD_CASE(1, 64, 1)
     FD_CASE(2, 16, 1) FD_CASE(2, 8, 3) FD_CASE(2, 32, 1) FD_CASE(2, 16, 3) FD_CASE(2, 64, 1)
 #undef FD_CASE
@@ -261,25 +254,18 @@ bool fused_shape_ok(int ni, int lo, int no) {
            (lo == 64 && no == 1);
 }
 
-int cu_count() {
-    static int n = 0;
-    if (!n) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            n = 0;
-    }
-    return n;
-}
-
 }  // namespace
 
-// Scratch bytes of the fused kernel: barrier words, logits, gate, the quantized down input
+namespace {
+size_t fa256(size_t v) { return (v + 255) & ~(size_t)255; }
+}
+
+// Scratch bytes of the three kernels: logits, gate, quantized x, routing, the quantized down input
 size_t moe_fused_scratch_bytes(const moe_layer_desc* d) {
     const int NS = d->n_used + (d->s_gate ? 1 : 0);
-    auto a256 = [](size_t v) { return (v + 255) & ~(size_t)255; };
-    return a256(16) + a256((size_t)d->n_expert * 4) + a256(4) + a256((size_t)NS * d->n_ff) +
-           a256((size_t)NS * d->n_ff / 32 * 4);
+    const size_t E = d->n_embd;
+    return fa256((size_t)d->n_expert * 4) + fa256(4) + fa256(E) + fa256(E / 32 * 4) + 2 * fa256(64 * 4) +
+           fa256((size_t)NS * d->n_ff) + fa256((size_t)NS * d->n_ff / 32 * 4);
 }
 
 // Whether the fused kernel takes this layer at T = 1: a Q8_0-activation type, every expert matrix registered in
@@ -293,7 +279,7 @@ bool moe_fused_prepare(const moe_layer_desc* d, FArgs& a) {
     moe_mv_shape(type, FE, &lo, &no);
     if (li != 64 || !fused_shape_ok(ni, lo, no)) return false;
     const int NS = NU + (d->s_gate ? 1 : 0);
-    if (NS > 16 || cu_count() == 0) return false;
+    if (NS > 16 || E % FD_RB) return false;
     const size_t rb_in = (size_t)E / 32 * (type == QT_Q8_0 ? 34 : type == QT_ROCMFP4 ? 18 : 17);
     const size_t rb_out = (size_t)FE / 32 * (type == QT_Q8_0 ? 34 : type == QT_ROCMFP4 ? 18 : 17);
     const void* W[6] = {d->w_gate, d->w_up, d->w_down, d->s_gate, d->s_up, d->s_down};
@@ -322,31 +308,42 @@ bool moe_fused_prepare(const moe_layer_desc* d, FArgs& a) {
 }
 
 hipError_t moe_fused_launch(const moe_layer_desc* d, FArgs& a, void* scratch, hipStream_t st) {
-    auto a256 = [](size_t v) { return (v + 255) & ~(size_t)255; };
     char* p = (char*)scratch;
-    a.bar = (unsigned*)p;
-    p += a256(16);
     a.logits = (float*)p;
-    p += a256((size_t)a.NE * 4);
+    p += fa256((size_t)a.NE * 4);
     a.sg = (float*)p;
-    p += a256(4);
+    p += fa256(4);
+    a.xq = (int8_t*)p;
+    p += fa256((size_t)a.E);
+    a.xd = (float*)p;
+    p += fa256((size_t)a.E / 32 * 4);
+    a.ids = (int*)p;
+    p += fa256(64 * 4);
+    a.wts = (float*)p;
+    p += fa256(64 * 4);
     a.act_q = (int8_t*)p;
-    p += a256((size_t)a.NS * a.FE);
+    p += fa256((size_t)a.NS * a.FE);
     a.act_d = (float*)p;
     int li, ni, lo, no;
     moe_mv_shape(d->type, a.E, &li, &ni);
     moe_mv_shape(d->type, a.FE, &lo, &no);
-    const int nblocks = cu_count();
     switch (d->type) {
-    case QT_Q8_0: return launch_fused_t<QT_Q8_0>(a, ni, lo, no, nblocks, st);
-    case QT_ROCMFP4: return launch_fused_t<QT_ROCMFP4>(a, ni, lo, no, nblocks, st);
-    default: return launch_fused_t<QT_ROCMFP4_FAST>(a, ni, lo, no, nblocks, st);
+    case QT_Q8_0: return launch_fused_t<QT_Q8_0>(a, ni, lo, no, st);
+    case QT_ROCMFP4: return launch_fused_t<QT_ROCMFP4>(a, ni, lo, no, st);
+    default: return launch_fused_t<QT_ROCMFP4_FAST>(a, ni, lo, no, st);
     }
 }
+
+static unsigned long long* g_stamps = nullptr;
+
+// Profiling: every later fused layer writes timestamps to stamps (device memory of 6 words per workgroup of the
+// largest of the three grids; nullptr: stop)
+extern "C" void moe_layer_fused_stamps(void* stamps) { g_stamps = (unsigned long long*)stamps; }
 
 bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits, float* out, int* ids_out,
                    float* wts_out, void* scratch, hipStream_t st, hipError_t* err) {
     FArgs a = {};
+    a.stamps = g_stamps;
     if (!moe_fused_prepare(d, a)) return false;
     a.x = x;
     a.logits_in = logits;

@@ -52,7 +52,7 @@ Plan plan(const moe_layer_desc* d, int T) {
     p.qx_k = r256((long long)T * E);
     p.qa_k = r256((long long)T * p.NS * FE);
     p.qs_k = r256((long long)T * FE);
-    size_t o = a256(p.fused);  // the fused kernel's region first: its barrier words open the scratch
+    size_t o = a256(p.fused);  // the fused kernels' region first
     auto take = [&](size_t bytes) {
         const size_t at = o;
         o += a256(bytes);
@@ -92,12 +92,6 @@ Plan plan(const moe_layer_desc* d, int T) {
 }  // namespace
 
 extern "C" void moe_layer_set_fused(int enable) { g_fused.store(enable ? 1 : 0); }
-
-extern "C" int moe_layer_fused_error(const void* scratch) {
-    unsigned w[3] = {0, 0, 0};
-    if (!scratch || hipMemcpy(w, scratch, sizeof(w), hipMemcpyDeviceToHost) != hipSuccess) return -1;
-    return (int)w[2];
-}
 
 extern "C" size_t moe_layer_scratch_bytes(const moe_layer_desc* d, int max_t) {
     if (!d || max_t <= 0) return 0;

@@ -73,7 +73,7 @@ SIGNATURES = {
     "moe_layer_scratch_bytes": (_Z, [ctypes.c_void_p, _I]),
     "moe_layer_forward": (_I, [ctypes.c_void_p, _P, _P, _I, _P, _P, _P, _P, _Z, _P]),
     "moe_layer_set_fused": (None, [_I]),
-    "moe_layer_fused_error": (_I, [_P]),
+    "moe_layer_fused_stamps": (None, [_P]),
 }
 
 
@@ -120,8 +120,7 @@ class MoeLib:
         def call(*args):
             r = fn(*args)
             if fn.restype is _I and name not in ("qmatvec_supported", "qmatvec_q8_supported", "qmatvec_id_batch_tile",
-                                                 "qmatvec_q8_id_batch_supported", "qmatvec_set_out_scale",
-                                                 "moe_layer_fused_error") and r != 0:
+                                                 "qmatvec_q8_id_batch_supported", "qmatvec_set_out_scale") and r != 0:
                 raise HipError(f"{name} returned hipError {r}")
             return r
         return call
