@@ -119,9 +119,6 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
 // ---- kernel 2: routing, then gate / up / SwiGLU / quantize of unit (slot, 32-row block)
 template <int TYPE, int NUPL_IN>
 __global__ void __launch_bounds__(256) k_fd_gate_up(FArgs a) {
-    __shared__ __attribute__((aligned(16))) float sl[ROUTER_MAX_E];
-    __shared__ float part[4];
-    __shared__ float sel_p[64];
     __shared__ int s_ids[65];
     __shared__ float s_wts[64];
     __shared__ float gu[2][32];
@@ -129,7 +126,7 @@ __global__ void __launch_bounds__(256) k_fd_gate_up(FArgs a) {
     const int FE = a.FE, NU = a.NU, nbf = FE / 32;
     const int slot = blockIdx.x / nbf, b = blockIdx.x - slot * nbf;
     stamp(a, 1);
-    router_select(a.logits_in ? a.logits_in : a.logits, a.NE, NU, sl, part, sel_p, s_ids, s_wts);
+    router_select(a.logits_in ? a.logits_in : a.logits, a.NE, NU, s_ids, s_wts);
     if (blockIdx.x == 0 && tid < NU) {  // the routing for kernel 3 and the caller
         a.ids[tid] = s_ids[tid];
         a.wts[tid] = s_wts[tid];

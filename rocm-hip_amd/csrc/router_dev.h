@@ -54,47 +54,93 @@ __device__ __forceinline__ float shexp_gate(const float* xr, const float* w, int
     return 1.0f / (1.0f + expf(-d));
 }
 
-// Softmax over ne logits, the nu largest in descending order (ties to the lower index), weights renormalised by
-// max(sum, 6.103515625e-5). sl: LDS of ROUTER_MAX_E floats; sel_p: LDS of 64. Writes id_row[0..nu) (any memory)
-// and, from thread 0, wts[0..nu). Selection by rank counting: an expert's rank is the number of experts with a
-// larger logit or an equal one at a lower index (softmax is strictly monotonic, so this is the probability order).
-__device__ __forceinline__ void router_select(const float* lg, int ne, int nu, float* sl, float* part, float* sel_p,
-                                              int* id_row, float* wts) {
-    const int tid = threadIdx.x;
-    for (int e = tid; e < ne; e += 256) sl[e] = lg[e];
-    const int ne4 = (ne + 3) & ~3;
-    for (int e = ne + tid; e < ne4; e += 256) sl[e] = -INFINITY;  // pad: never beats a real expert
+// Order-preserving map of a float onto uint32 (larger float, larger key; -0 below +0)
+__device__ __forceinline__ uint32_t f32_order_key(float v) {
+    const uint32_t u = __float_as_uint(v);
+    return u ^ ((u >> 31) ? 0xffffffffu : 0x80000000u);
+}
+
+__device__ __forceinline__ float f32_from_order_key(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? k ^ 0x80000000u : ~k);
+}
+
+// Largest 64-bit key over the wave, in every lane
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+#define RS_STEP(S)                                                                              \
+    {                                                                                           \
+        const uint32_t lo = (uint32_t)partner_i<S>((int)(uint32_t)k);                           \
+        const uint32_t hi = (uint32_t)partner_i<S>((int)(uint32_t)(k >> 32));                   \
+        const uint64_t o = ((uint64_t)hi << 32) | lo;                                           \
+        k = o > k ? o : k;                                                                      \
+    }
+    RS_STEP(1) RS_STEP(2) RS_STEP(4) RS_STEP(8) RS_STEP(16) RS_STEP(32)
+#undef RS_STEP
+    return k;
+}
+
+// Selection on one wave; lane l holds logits l, l + 64, ... (NPL of them). Key: the logit's order key above the
+// complement of its index, so the largest key is the largest logit, ties to the lower index; a taken (or absent)
+// entry has key 0, below every real one.
+template <int NPL>
+__device__ __forceinline__ void router_select_wave(const float* lg, int ne, int nu, int* id_row, float* wts) {
+    const int lane = threadIdx.x & 63;
+    float v[NPL];
+    uint64_t key[NPL];
     float mx = -INFINITY;
-    for (int e = tid; e < ne; e += 256) mx = fmaxf(mx, lg[e]);
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = e < ne ? lg[e] : -INFINITY;
+        key[j] = e < ne ? ((uint64_t)f32_order_key(v[j]) << 32) | (0xffffffffu - (uint32_t)e) : 0;
+        mx = fmaxf(mx, v[j]);
+    }
     mx = wave_max(mx);
-    if ((tid & 63) == 0) part[tid >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
-    __syncthreads();
     float sum = 0.0f;
-    for (int e = tid; e < ne; e += 256) sum += expf(sl[e] - mx);
-    sum = block256_sum(sum, part);
+#pragma unroll
+    for (int j = 0; j < NPL; ++j)
+        if (lane + 64 * j < ne) sum += expf(v[j] - mx);
+    sum = wave_sum(sum);
     const float inv = 1.0f / sum;
-    for (int e = tid; e < ne; e += 256) {
-        const float v = sl[e];
-        int rank = 0;
-        for (int k = 0; k < ne4; k += 4) {
-            const float4 c = *(const float4*)(sl + k);
-            rank += (c.x > v || (c.x == v && k < e)) + (c.y > v || (c.y == v && k + 1 < e)) +
-                    (c.z > v || (c.z == v && k + 2 < e)) + (c.w > v || (c.w == v && k + 3 < e));
+    float ws = 0.0f, myp = 0.0f;
+    int myid = 0;
+    for (int r = 0; r < nu; ++r) {
+        uint64_t best = key[0];
+#pragma unroll
+        for (int j = 1; j < NPL; ++j) best = key[j] > best ? key[j] : best;
+        best = wave_max_u64(best);
+#pragma unroll
+        for (int j = 0; j < NPL; ++j)
+            if (key[j] == best) key[j] = 0;
+        const int e = (int)(0xffffffffu - (uint32_t)best);
+        const float p = expf(f32_from_order_key((uint32_t)(best >> 32)) - mx) * inv;
+        ws += p;  // the sum in rank order
+        if (lane == r) {
+            myp = p;
+            myid = e;
         }
-        if (rank < nu) {
-            id_row[rank] = e;
-            sel_p[rank] = expf(v - mx) * inv;
-        }
+    }
+    ws = fmaxf(ws, 6.103515625e-5f);
+    if (lane < nu) {
+        id_row[lane] = myid;
+        wts[lane] = myp / ws;
+    }
+}
+
+// Softmax over ne (<= ROUTER_MAX_E) logits, the nu (<= 64) largest in descending order (ties to the lower index),
+// weights renormalised by max(sum, 6.103515625e-5). Wave 0 of the 256-thread workgroup selects; it writes
+// id_row[0..nu) and wts[0..nu) (any memory), visible to the whole workgroup on return.
+__device__ __forceinline__ void router_select(const float* lg, int ne, int nu, int* id_row, float* wts) {
+    if (threadIdx.x < 64) {
+        if (ne <= 128)
+            router_select_wave<2>(lg, ne, nu, id_row, wts);
+        else if (ne <= 256)
+            router_select_wave<4>(lg, ne, nu, id_row, wts);
+        else if (ne <= 512)
+            router_select_wave<8>(lg, ne, nu, id_row, wts);
+        else
+            router_select_wave<16>(lg, ne, nu, id_row, wts);
     }
     __syncthreads();
-    if (tid == 0) {
-        float ws = 0.0f;
-        for (int r = 0; r < nu; ++r) ws += sel_p[r];
-        ws = fmaxf(ws, 6.103515625e-5f);
-        for (int r = 0; r < nu; ++r) wts[r] = sel_p[r] / ws;
-    }
 }
 
 #endif  // ROUTER_DEV_H

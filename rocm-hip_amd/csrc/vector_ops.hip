@@ -183,16 +183,14 @@ __global__ void __launch_bounds__(256) k_matmul_f32(const float* W, long long ld
 // One 256-thread workgroup per token: the shared-expert gate, then router_select (router_dev.h).
 __global__ void __launch_bounds__(256) k_router(const float* logits, const float* x, const float* w_shexp, int* ids,
                                                 float* wts, float* sg, int ne, int nu, int n, int ids_stride) {
-    __shared__ __attribute__((aligned(16))) float sl[ROUTER_MAX_E];
     __shared__ float part[4];
-    __shared__ float sel_p[64];
     const int t = blockIdx.x, tid = threadIdx.x;
     if (w_shexp) {  // (uniform branch)
         const float g = shexp_gate(x + (size_t)t * n, w_shexp, n, part);
         if (tid == 0) sg[t] = g;
     }
     int* id_row = ids + (size_t)t * ids_stride;
-    router_select(logits + (size_t)t * ne, ne, nu, sl, part, sel_p, id_row, wts + (size_t)t * nu);
+    router_select(logits + (size_t)t * ne, ne, nu, id_row, wts + (size_t)t * nu);
     if (tid == 0 && ids_stride > nu) id_row[nu] = -1;
 }
 
