@@ -50,9 +50,9 @@ hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x, const floa
 void moe_layer_set_fused(int enable);
 
 // No counterpart in the reference (its QWEN_PROFILE times sections on the host). Profiling: every later fused
-// layer writes wall-clock stamps (100 MHz) per workgroup to stamps: [workgroup][6], kernel 1 in column 0,
-// kernel 2 in 1..3 (start, routed, done), kernel 3 in 4, 5; rows for the largest grid (max(NE + 1, NS * FE / 32,
-// E / 8)); NULL stops.
+// layer writes wall-clock stamps (100 MHz) per workgroup to stamps: [workgroup][8], kernel 1 in columns 0, 1
+// (start, done), kernel 2 in 2..4 (start, routed, done), kernel 3 in 5, 6; rows for the largest grid
+// (max(NE + 1, NS * FE / 32, E) always suffices); NULL stops. Launches capture the pointer current at the call.
 void moe_layer_fused_stamps(void* stamps);
 
 #ifdef __cplusplus

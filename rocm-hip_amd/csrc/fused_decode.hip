@@ -8,7 +8,8 @@
 //   2  one workgroup per (slot, 32-row block of FE): it routes (the router's own code on the logits, every
 //      workgroup for itself; workgroup 0 also publishes ids / weights), then computes the slot expert's 32 gate
 //      and 32 up rows, SwiGLU, and the Q8_0 quantization of those 32 values (one Q8_0 block of down's input);
-//   3  one workgroup per 8 output rows: their down rows for every slot, then the combine in slot order.
+//   3  one workgroup per 64 / L output rows (L: the down row dot's lanes), one wave per slot: their down rows,
+//      then the combine in slot order.
 // Every sum is formed in the same order as the per-operation kernels (rows_dot's lane groups and DPP group sums,
 // the same router, quantizer and combine), so the layer's output equals the per-operation path bit for bit.
 // (A single persistent kernel with two grid barriers was measured slower: each barrier's cross-XCD fences and
@@ -21,7 +22,6 @@
 #include "router_dev.h"
 
 #define FD_MAX_E 4096
-#define FD_RB 8                 // output rows per down unit
 
 struct FArgs {
     const float* x;          // [E]
@@ -46,28 +46,31 @@ struct FArgs {
     int E, NE, NU, FE, NS, has_gate;
 };
 
-// Timestamp k of this workgroup (the 100 MHz wall clock), when stamps are requested: kernel 1 uses slots 0,
-// kernel 2 slots 1..3, kernel 3 slots 4, 5 of row blockIdx.x of a [max grid][6] table
+// Timestamp k of this workgroup (the 100 MHz wall clock), when stamps are requested: kernel 1 uses slots 0, 1,
+// kernel 2 slots 2..4, kernel 3 slots 5, 6 of row blockIdx.x of a [max grid][8] table
 __device__ __forceinline__ void stamp(const FArgs& a, int k) {
-    if (a.stamps && threadIdx.x == 0) a.stamps[blockIdx.x * 6 + k] = wall_clock64();
+    if (a.stamps && threadIdx.x == 0) a.stamps[blockIdx.x * 8 + k] = wall_clock64();
 }
 
 // The down phase's row dots: R row dots per lane group of L lanes, each with its own weight row and input row;
 // all loads first, then the units in ascending order per row (rows_dot's order), then the group sums
+// (only rows r < nvalid are loaded; the others' results are undefined)
 template <int TYPE, int L, int R, int NUPL>
 __device__ __forceinline__ void rows_dot_multi(const uint8_t* const vr[R], const uint8_t* const sr[R],
                                                const int8_t* const xq[R], const float* const xd[R], int nu, int gl,
-                                               float acc[R]) {
+                                               int nvalid, float acc[R]) {
     WUnit<TYPE> w[R][NUPL];
     XUnit<TYPE> x[R][NUPL];
 #pragma unroll
     for (int r = 0; r < R; ++r)
+        if (r < nvalid)
 #pragma unroll
-        for (int i = 0; i < NUPL; ++i) load_packed<TYPE>(vr[r], sr[r], gl + i * L, nu, w[r][i]);
+            for (int i = 0; i < NUPL; ++i) load_packed<TYPE>(vr[r], sr[r], gl + i * L, nu, w[r][i]);
 #pragma unroll
     for (int r = 0; r < R; ++r)
+        if (r < nvalid)
 #pragma unroll
-        for (int i = 0; i < NUPL; ++i) load_x<TYPE>(xq[r], xd[r], nullptr, gl + i * L, x[r][i]);
+            for (int i = 0; i < NUPL; ++i) load_x<TYPE>(xq[r], xd[r], nullptr, gl + i * L, x[r][i]);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         acc[r] = 0.0f;
@@ -85,6 +88,7 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
     if ((int)blockIdx.x < a.NE) {
         const float y = f32_row_dot(a.w_router + (size_t)blockIdx.x * E, a.x, E, part);
         if (tid == 0) a.logits[blockIdx.x] = y;
+        stamp(a, 1);
         return;
     }
     // Q8_0 per 32 values (4 threads of 8 values): the quantizer's expressions
@@ -114,6 +118,7 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
         const float g = shexp_gate(a.x, a.w_shexp, E, part);
         if (tid == 0) a.sg[0] = g;
     }
+    stamp(a, 1);
 }
 
 // ---- kernel 2: routing, then gate / up / SwiGLU / quantize of unit (slot, 32-row block)
@@ -125,7 +130,7 @@ __global__ void __launch_bounds__(256) k_fd_gate_up(FArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int FE = a.FE, NU = a.NU, nbf = FE / 32;
     const int slot = blockIdx.x / nbf, b = blockIdx.x - slot * nbf;
-    stamp(a, 1);
+    stamp(a, 2);
     router_select(a.logits_in ? a.logits_in : a.logits, a.NE, NU, s_ids, s_wts);
     if (blockIdx.x == 0 && tid < NU) {  // the routing for kernel 3 and the caller
         a.ids[tid] = s_ids[tid];
@@ -133,7 +138,7 @@ __global__ void __launch_bounds__(256) k_fd_gate_up(FArgs a) {
         if (a.ids_out) a.ids_out[tid] = s_ids[tid];
         if (a.wts_out) a.wts_out[tid] = s_wts[tid];
     }
-    stamp(a, 2);
+    stamp(a, 3);
     const int e = slot < NU ? s_ids[slot] : -1;
     const int mat = w >> 1;  // waves 0, 1: gate rows; 2, 3: up rows
     const int mi = e >= 0 ? mat : 3 + mat;
@@ -158,63 +163,39 @@ __global__ void __launch_bounds__(256) k_fd_gate_up(FArgs a) {
             if (t == 0) a.act_d[(long long)slot * nbf + b] = __half2float(__float2half(am / 127.0f));
         }
     }
-    stamp(a, 3);
+    stamp(a, 4);
 }
 
-// ---- kernel 3: down rows of every slot for FD_RB output rows, then the combine in slot order. Lane groups of
-// L_OUT lanes with NUPL_OUT units each: the per-operation down kernel's shape for this K, so the same sums.
+// ---- kernel 3: down rows of every slot for RB = 64 / L_OUT output rows, then the combine in slot order. One wave
+// per slot, one lane group of L_OUT lanes (NUPL_OUT units each) per output row: the per-operation down kernel's
+// shape for this K, so the same sums.
 template <int TYPE, int L_OUT, int NUPL_OUT>
-__global__ void __launch_bounds__(256) k_fd_down(FArgs a) {
-    __shared__ int s_ids[65];
-    __shared__ float s_wts[64];
-    __shared__ float downv[16][FD_RB];
+__global__ void __launch_bounds__(1024) k_fd_down(FArgs a) {
+    constexpr int RB = 64 / L_OUT;
+    __shared__ float downv[16][RB];
     const int tid = threadIdx.x, E = a.E, FE = a.FE, NU = a.NU, NS = a.NS;
-    stamp(a, 4);
-    if (tid < NU) {
-        s_ids[tid] = a.ids[tid];
-        s_wts[tid] = a.wts[tid];
-    }
-    if (tid == 0) s_ids[NU] = -1;  // the shared expert's slot
+    const int slot = tid >> 6, lane = tid & 63, gl = lane & (L_OUT - 1), i = lane / L_OUT;
+    const int i0 = blockIdx.x * RB;
+    stamp(a, 5);
+    const int e = slot < NU ? a.ids[slot] : -1;
+    const long long row = e >= 0 ? (long long)e * E + i0 + i : i0 + i;
+    const int mi = e >= 0 ? 2 : 5;
+    const uint8_t* vr[1] = {a.v[mi] + row * a.vrb_out};
+    const uint8_t* sr[1] = {a.s[mi] + row * a.srb_out};
+    const int8_t* xq[1] = {a.act_q + (long long)slot * FE};
+    const float* xd[1] = {a.act_d + (long long)slot * (FE / 32)};
+    float acc[1];
+    rows_dot_multi<TYPE, L_OUT, 1, NUPL_OUT>(vr, sr, xq, xd, FE / 32, gl, 1, acc);
+    if (gl == 0) downv[slot][i] = acc[0];
     __syncthreads();
-    constexpr int NG = 256 / L_OUT;  // lane groups per workgroup
-    constexpr int RR = 4;            // row dots per group and round
-    const int gl = tid & (L_OUT - 1), grp = tid / L_OUT;
-    const int ndots = NS * FD_RB;
-    const int i0 = blockIdx.x * FD_RB;
-    for (int k0 = 0; k0 < ndots; k0 += NG * RR) {
-        const uint8_t* vr[RR];
-        const uint8_t* sr[RR];
-        const int8_t* xq[RR];
-        const float* xd[RR];
-#pragma unroll
-        for (int r = 0; r < RR; ++r) {
-            const int k = min(k0 + grp + NG * r, ndots - 1);  // idle row dots repeat the last one (not stored)
-            const int slot = k / FD_RB, i = k - slot * FD_RB;
-            const int e = s_ids[slot];
-            const long long row = e >= 0 ? (long long)e * E + i0 + i : i0 + i;
-            const int mi = e >= 0 ? 2 : 5;
-            vr[r] = a.v[mi] + row * a.vrb_out;
-            sr[r] = a.s[mi] + row * a.srb_out;
-            xq[r] = a.act_q + (long long)slot * FE;
-            xd[r] = a.act_d + (long long)slot * (FE / 32);
-        }
-        float acc[RR];
-        rows_dot_multi<TYPE, L_OUT, RR, NUPL_OUT>(vr, sr, xq, xd, FE / 32, gl, acc);
-        if (gl == 0)
-#pragma unroll
-            for (int r = 0; r < RR; ++r) {
-                const int k = k0 + grp + NG * r;
-                if (k < ndots) downv[k / FD_RB][k % FD_RB] = acc[r];
-            }
-    }
-    __syncthreads();
-    if (tid < FD_RB) {  // the combine kernel's expression
-        float o = s_wts[0] * downv[0][tid];
-        for (int j = 1; j < NU; ++j) o += s_wts[j] * downv[j][tid];
+    if (tid < RB) {  // the combine kernel's expression
+        const float* wts = a.wts;
+        float o = wts[0] * downv[0][tid];
+        for (int j = 1; j < NU; ++j) o += wts[j] * downv[j][tid];
         if (NS > NU) o += a.has_gate ? downv[NU][tid] * a.sg[0] : downv[NU][tid];
         a.out[i0 + tid] = o;
     }
-    stamp(a, 5);
+    stamp(a, 6);
 }
 
 // ------------------------------------------------------------------ host side
@@ -229,7 +210,7 @@ hipError_t launch_fused(const FArgs& a, hipStream_t st) {
     hipError_t e = launch_kernel(k_fd_logits, dim3(a.NE + 1), dim3(256), 0, st, a);
     if (e == hipSuccess)
         e = launch_kernel(k_fd_gate_up<TYPE, NI>, dim3(a.NS * (a.FE / 32)), dim3(256), 0, st, a);
-    if (e == hipSuccess) e = launch_kernel(k_fd_down<TYPE, LO, NO>, dim3(a.E / FD_RB), dim3(256), 0, st, a);
+    if (e == hipSuccess) e = launch_kernel(k_fd_down<TYPE, LO, NO>, dim3(a.E / (64 / LO)), dim3(64 * a.NS), 0, st, a);
     return e;
 }
 
@@ -276,7 +257,7 @@ bool moe_fused_prepare(const moe_layer_desc* d, FArgs& a) {
     moe_mv_shape(type, FE, &lo, &no);
     if (li != 64 || !fused_shape_ok(ni, lo, no)) return false;
     const int NS = NU + (d->s_gate ? 1 : 0);
-    if (NS > 16 || E % FD_RB) return false;
+    if (NS > 16) return false;
     const size_t rb_in = (size_t)E / 32 * (type == QT_Q8_0 ? 34 : type == QT_ROCMFP4 ? 18 : 17);
     const size_t rb_out = (size_t)FE / 32 * (type == QT_Q8_0 ? 34 : type == QT_ROCMFP4 ? 18 : 17);
     const void* W[6] = {d->w_gate, d->w_up, d->w_down, d->s_gate, d->s_up, d->s_down};
@@ -333,7 +314,7 @@ hipError_t moe_fused_launch(const moe_layer_desc* d, FArgs& a, void* scratch, hi
 
 static unsigned long long* g_stamps = nullptr;
 
-// Profiling: every later fused layer writes timestamps to stamps (device memory of 6 words per workgroup of the
+// Profiling: every later fused layer writes timestamps to stamps (device memory of 8 words per workgroup of the
 // largest of the three grids; nullptr: stop)
 extern "C" void moe_layer_fused_stamps(void* stamps) { g_stamps = (unsigned long long*)stamps; }
 
