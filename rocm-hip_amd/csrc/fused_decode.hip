@@ -3,8 +3,8 @@
 // The per-operation layer (router logits, router, quantize, gate/up, SwiGLU, down, combine) costs seven launches,
 // each with ~2.5 us of ramp and tail on MI355X, while the layer's ~25-40 MB of weights take 3-5 us at HBM speed.
 // Here the layer is three launches with no grid-wide synchronisation inside any of them:
-//   1  one workgroup per router-logit row, plus one that quantizes x (the activation quantizer's expressions)
-//      and computes the shared-expert gate;
+//   1  one workgroup per router-logit row, one that quantizes x (the activation quantizer's expressions) and
+//      one for the shared-expert gate;
 //   2  one workgroup per (slot, 32-row block of FE): it routes (the router's own code on the logits, every
 //      workgroup for itself; workgroup 0 also publishes ids / weights), then computes the slot expert's 32 gate
 //      and 32 up rows, SwiGLU, and the Q8_0 quantization of those 32 values (one Q8_0 block of down's input);
@@ -80,7 +80,7 @@ __device__ __forceinline__ void rows_dot_multi(const uint8_t* const vr[R], const
     }
 }
 
-// ---- kernel 1: router logits (workgroups 0 .. NE - 1), x quantized + the shared gate (workgroup NE)
+// ---- kernel 1: router logits (workgroups 0 .. NE - 1), x quantized (workgroup NE), the shared gate (NE + 1)
 __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
     __shared__ float part[4];
     const int tid = threadIdx.x, E = a.E;
@@ -88,6 +88,12 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
     if ((int)blockIdx.x < a.NE) {
         const float y = f32_row_dot(a.w_router + (size_t)blockIdx.x * E, a.x, E, part);
         if (tid == 0) a.logits[blockIdx.x] = y;
+        stamp(a, 1);
+        return;
+    }
+    if ((int)blockIdx.x == a.NE + 1) {  // the shared expert's gate
+        const float g = shexp_gate(a.x, a.w_shexp, E, part);
+        if (tid == 0) a.sg[0] = g;
         stamp(a, 1);
         return;
     }
@@ -113,10 +119,6 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
                                                   ((uint32_t)q[7] << 24));
             if ((tid & 3) == 0) a.xd[i0 / 32] = __half2float(__float2half(am / 127.0f));
         }
-    }
-    if (a.has_gate) {
-        const float g = shexp_gate(a.x, a.w_shexp, E, part);
-        if (tid == 0) a.sg[0] = g;
     }
     stamp(a, 1);
 }
@@ -207,7 +209,7 @@ namespace {
 
 template <int TYPE, int NI, int LO, int NO>
 hipError_t launch_fused(const FArgs& a, hipStream_t st) {
-    hipError_t e = launch_kernel(k_fd_logits, dim3(a.NE + 1), dim3(256), 0, st, a);
+    hipError_t e = launch_kernel(k_fd_logits, dim3(a.NE + 1 + a.has_gate), dim3(256), 0, st, a);
     if (e == hipSuccess)
         e = launch_kernel(k_fd_gate_up<TYPE, NI>, dim3(a.NS * (a.FE / 32)), dim3(256), 0, st, a);
     if (e == hipSuccess) e = launch_kernel(k_fd_down<TYPE, LO, NO>, dim3(a.E / (64 / LO)), dim3(64 * a.NS), 0, st, a);

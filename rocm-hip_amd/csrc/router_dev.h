@@ -54,44 +54,56 @@ __device__ __forceinline__ float shexp_gate(const float* xr, const float* w, int
     return 1.0f / (1.0f + expf(-d));
 }
 
-// Order-preserving map of a float onto uint32 (larger float, larger key; -0 below +0)
+// Order-preserving map of a float onto uint32 (larger float, larger key; keys of real floats are >= 0x007fffff)
 __device__ __forceinline__ uint32_t f32_order_key(float v) {
     const uint32_t u = __float_as_uint(v);
     return u ^ ((u >> 31) ? 0xffffffffu : 0x80000000u);
 }
-
 __device__ __forceinline__ float f32_from_order_key(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? k ^ 0x80000000u : ~k);
 }
 
-// Largest 64-bit key over the wave, in every lane
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
-#define RS_STEP(S)                                                                              \
-    {                                                                                           \
-        const uint32_t lo = (uint32_t)partner_i<S>((int)(uint32_t)k);                           \
-        const uint32_t hi = (uint32_t)partner_i<S>((int)(uint32_t)(k >> 32));                   \
-        const uint64_t o = ((uint64_t)hi << 32) | lo;                                           \
-        k = o > k ? o : k;                                                                      \
-    }
-    RS_STEP(1) RS_STEP(2) RS_STEP(4) RS_STEP(8) RS_STEP(16) RS_STEP(32)
-#undef RS_STEP
-    return k;
+// Wave-wide unsigned max / min, read out of lane 63 as a wave-uniform value: the row steps (quad, half-row and row
+// mirrors leave every lane of a 16-lane row with the row's result), then row_bcast:15 and row_bcast:31 carry rows
+// 0..2 into lane 63. Each step is one DPP-operand VALU op (the operation's identity fills lanes a step skips).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v, uint32_t identity) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
+__device__ __forceinline__ uint32_t wave_max_u32_uniform(uint32_t v) {
+    v = max(v, dpp_u<0xb1, 0xf>(v, 0u));
+    v = max(v, dpp_u<0x4e, 0xf>(v, 0u));
+    v = max(v, dpp_u<0x141, 0xf>(v, 0u));
+    v = max(v, dpp_u<0x140, 0xf>(v, 0u));
+    v = max(v, dpp_u<0x142, 0xa>(v, 0u));
+    v = max(v, dpp_u<0x143, 0xc>(v, 0u));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+__device__ __forceinline__ uint32_t wave_min_u32_uniform(uint32_t v) {
+    v = min(v, dpp_u<0xb1, 0xf>(v, 0xffffffffu));
+    v = min(v, dpp_u<0x4e, 0xf>(v, 0xffffffffu));
+    v = min(v, dpp_u<0x141, 0xf>(v, 0xffffffffu));
+    v = min(v, dpp_u<0x140, 0xf>(v, 0xffffffffu));
+    v = min(v, dpp_u<0x142, 0xa>(v, 0xffffffffu));
+    v = min(v, dpp_u<0x143, 0xc>(v, 0xffffffffu));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-// Selection on one wave; lane l holds logits l, l + 64, ... (NPL of them). Key: the logit's order key above the
-// complement of its index, so the largest key is the largest logit, ties to the lower index; a taken (or absent)
-// entry has key 0, below every real one.
+// Selection on one wave; lane l holds logits l, l + 64, ... (NPL of them) as order keys (0: taken or absent, below
+// every real key; -0 is keyed as +0). Each of the nu rounds takes the largest remaining key (a max reduction), then
+// the lowest index holding it (a min reduction), so ties go to the lower index. Lane r keeps round r's logit and
+// index; the probabilities and their sum in rank order follow the rounds.
 template <int NPL>
 __device__ __forceinline__ void router_select_wave(const float* lg, int ne, int nu, int* id_row, float* wts) {
     const int lane = threadIdx.x & 63;
     float v[NPL];
-    uint64_t key[NPL];
+    uint32_t key[NPL];
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
         const int e = lane + 64 * j;
         v[j] = e < ne ? lg[e] : -INFINITY;
-        key[j] = e < ne ? ((uint64_t)f32_order_key(v[j]) << 32) | (0xffffffffu - (uint32_t)e) : 0;
+        key[j] = e < ne ? f32_order_key(v[j] == 0.0f ? 0.0f : v[j]) : 0u;
         mx = fmaxf(mx, v[j]);
     }
     mx = wave_max(mx);
@@ -101,28 +113,33 @@ __device__ __forceinline__ void router_select_wave(const float* lg, int ne, int 
         if (lane + 64 * j < ne) sum += expf(v[j] - mx);
     sum = wave_sum(sum);
     const float inv = 1.0f / sum;
-    float ws = 0.0f, myp = 0.0f;
+    uint32_t mykey = 0;
     int myid = 0;
     for (int r = 0; r < nu; ++r) {
-        uint64_t best = key[0];
+        uint32_t lk = key[0];
 #pragma unroll
-        for (int j = 1; j < NPL; ++j) best = key[j] > best ? key[j] : best;
-        best = wave_max_u64(best);
+        for (int j = 1; j < NPL; ++j) lk = max(lk, key[j]);
+        const uint32_t best = wave_max_u32_uniform(lk);
+        uint32_t li = 0xffffffffu;
+#pragma unroll
+        for (int j = NPL - 1; j >= 0; --j)
+            if (key[j] == best) li = lane + 64 * j;
+        const uint32_t e = wave_min_u32_uniform(li);
 #pragma unroll
         for (int j = 0; j < NPL; ++j)
-            if (key[j] == best) key[j] = 0;
-        const int e = (int)(0xffffffffu - (uint32_t)best);
-        const float p = expf(f32_from_order_key((uint32_t)(best >> 32)) - mx) * inv;
-        ws += p;  // the sum in rank order
+            if (lane + 64 * j == (int)e) key[j] = 0u;
         if (lane == r) {
-            myp = p;
-            myid = e;
+            mykey = best;
+            myid = (int)e;
         }
     }
+    const float p = expf(f32_from_order_key(mykey) - mx) * inv;
+    float ws = 0.0f;
+    for (int r = 0; r < nu; ++r) ws += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), r));  // rank order
     ws = fmaxf(ws, 6.103515625e-5f);
     if (lane < nu) {
         id_row[lane] = myid;
-        wts[lane] = myp / ws;
+        wts[lane] = p / ws;
     }
 }
 
