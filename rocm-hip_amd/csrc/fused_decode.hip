@@ -22,6 +22,9 @@
 #include "router_dev.h"
 
 #define FD_MAX_E 4096
+#ifndef FD_GU_RW
+#define FD_GU_RW 4              // gate / up rows per wave in kernel 2 (64 / FD_GU_RW waves per workgroup)
+#endif
 
 struct FArgs {
     const float* x;          // [E]
@@ -125,7 +128,8 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
 
 // ---- kernel 2: routing, then gate / up / SwiGLU / quantize of unit (slot, 32-row block)
 template <int TYPE, int NUPL_IN>
-__global__ void __launch_bounds__(256) k_fd_gate_up(FArgs a) {
+__global__ void __launch_bounds__(64 * (64 / FD_GU_RW)) k_fd_gate_up(FArgs a) {
+    constexpr int RW = FD_GU_RW, WPM = 32 / RW;  // rows per wave, waves per matrix
     __shared__ int s_ids[65];
     __shared__ float s_wts[64];
     __shared__ float gu[2][32];
@@ -142,17 +146,17 @@ __global__ void __launch_bounds__(256) k_fd_gate_up(FArgs a) {
     }
     stamp(a, 3);
     const int e = slot < NU ? s_ids[slot] : -1;
-    const int mat = w >> 1;  // waves 0, 1: gate rows; 2, 3: up rows
+    const int mat = w / WPM;  // the first WPM waves: gate rows; the next WPM: up rows
     const int mi = e >= 0 ? mat : 3 + mat;
     const long long rbase = e >= 0 ? (long long)e * FE : 0;
     const uint8_t* vb = a.v[mi] + rbase * a.vrb_in;
     const uint8_t* sb = a.s[mi] + rbase * a.srb_in;
-    float acc[16];
-    rows_dot<TYPE, true, 64, 16, NUPL_IN>(vb, sb, a.vrb_in, a.srb_in, 32 * b + 16 * (w & 1), 1, FE, a.xq, a.xd,
+    float acc[RW];
+    rows_dot<TYPE, true, 64, RW, NUPL_IN>(vb, sb, a.vrb_in, a.srb_in, 32 * b + RW * (w % WPM), 1, FE, a.xq, a.xd,
                                           nullptr, a.E, lane, acc);
     if (lane == 0)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) gu[mat][16 * (w & 1) + r] = acc[r];
+        for (int r = 0; r < RW; ++r) gu[mat][RW * (w % WPM) + r] = acc[r];
     __syncthreads();
     if (w == 0) {  // SwiGLU (the swiglu kernel's expression) and the Q8_0 block of these 32 values
         const int t = lane & 31;
@@ -211,7 +215,7 @@ template <int TYPE, int NI, int LO, int NO>
 hipError_t launch_fused(const FArgs& a, hipStream_t st) {
     hipError_t e = launch_kernel(k_fd_logits, dim3(a.NE + 1 + a.has_gate), dim3(256), 0, st, a);
     if (e == hipSuccess)
-        e = launch_kernel(k_fd_gate_up<TYPE, NI>, dim3(a.NS * (a.FE / 32)), dim3(256), 0, st, a);
+        e = launch_kernel(k_fd_gate_up<TYPE, NI>, dim3(a.NS * (a.FE / 32)), dim3(64 * (64 / FD_GU_RW)), 0, st, a);
     if (e == hipSuccess) e = launch_kernel(k_fd_down<TYPE, LO, NO>, dim3(a.E / (64 / LO)), dim3(64 * a.NS), 0, st, a);
     return e;
 }
