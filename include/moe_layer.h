@@ -46,8 +46,10 @@ hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x, const floa
                              int* ids_out, float* wts_out, void* scratch, size_t scratch_bytes, hipStream_t stream);
 
 // No counterpart in the reference. Whether T == 1 calls may use the fused kernels (1, the default) or always take
-// the per-operation launches (0); process-wide.
-void moe_layer_set_fused(int enable);
+// the per-operation launches (0); process-wide. Profiling only: 0x100 | mask launches just the fused kernels in
+// mask (bit 0: logits / quantize, bit 1: routing + gate / up, bit 2: down + combine), which then read what earlier
+// calls left in scratch; a layer's results are undefined in that mode. Other values select 1.
+void moe_layer_set_fused(int mode);
 
 // No counterpart in the reference (its QWEN_PROFILE times sections on the host). Profiling: every later fused
 // layer writes wall-clock stamps (100 MHz) per workgroup to stamps: [workgroup][8], kernel 1 in columns 0, 1

@@ -211,21 +211,24 @@ void moe_mv_shape(int type, int K, int* lanes, int* units_per_lane);
 
 namespace {
 
+// kernels: bit 0, 1, 2 launch kernel 1, 2, 3 (7 in normal use; a subset only for profiling one kernel)
 template <int TYPE, int NI, int LO, int NO>
-hipError_t launch_fused(const FArgs& a, hipStream_t st) {
-    hipError_t e = launch_kernel(k_fd_logits, dim3(a.NE + 1 + a.has_gate), dim3(256), 0, st, a);
-    if (e == hipSuccess)
+hipError_t launch_fused(const FArgs& a, int kernels, hipStream_t st) {
+    hipError_t e = hipSuccess;
+    if (kernels & 1) e = launch_kernel(k_fd_logits, dim3(a.NE + 1 + a.has_gate), dim3(256), 0, st, a);
+    if (e == hipSuccess && (kernels & 2))
         e = launch_kernel(k_fd_gate_up<TYPE, NI>, dim3(a.NS * (a.FE / 32)), dim3(64 * (64 / FD_GU_RW)), 0, st, a);
-    if (e == hipSuccess) e = launch_kernel(k_fd_down<TYPE, LO, NO>, dim3(a.E / (64 / LO)), dim3(64 * a.NS), 0, st, a);
+    if (e == hipSuccess && (kernels & 4))
+        e = launch_kernel(k_fd_down<TYPE, LO, NO>, dim3(a.E / (64 / LO)), dim3(64 * a.NS), 0, st, a);
     return e;
 }
 
 // Gate / up: 64 lanes per row, NI units per lane (K = E = 2048 or 4096). Down: the per-operation kernel's
 // (lanes, units) for K = FE: 512 -> (16, 1), 768 -> (8, 3), 1024 -> (32, 1), 1536 -> (16, 3), 2048 -> (64, 1).
 template <int TYPE>
-hipError_t launch_fused_t(const FArgs& a, int ni, int lo, int no, hipStream_t st) {
+hipError_t launch_fused_t(const FArgs& a, int ni, int lo, int no, int kernels, hipStream_t st) {
 #define FD_CASE(I, L, O) \
-    if (ni == I && lo == L && no == O) return launch_fused<TYPE, I, L, O>(a, st);
+    if (ni == I && lo == L && no == O) return launch_fused<TYPE, I, L, O>(a, kernels, st);
     FD_CASE(1, 16, 1) FD_CASE(1, 8, 3) FD_CASE(1, 32, 1) FD_CASE(1, 16, 3) FD_CASE(1, 64, 1)
     FD_CASE(2, 16, 1) FD_CASE(2, 8, 3) FD_CASE(2, 32, 1) FD_CASE(2, 16, 3) FD_CASE(2, 64, 1)
 #undef FD_CASE
@@ -291,7 +294,7 @@ bool moe_fused_prepare(const moe_layer_desc* d, FArgs& a) {
     return true;
 }
 
-hipError_t moe_fused_launch(const moe_layer_desc* d, FArgs& a, void* scratch, hipStream_t st) {
+hipError_t moe_fused_launch(const moe_layer_desc* d, FArgs& a, void* scratch, int kernels, hipStream_t st) {
     char* p = (char*)scratch;
     a.logits = (float*)p;
     p += fa256((size_t)a.NE * 4);
@@ -312,9 +315,9 @@ hipError_t moe_fused_launch(const moe_layer_desc* d, FArgs& a, void* scratch, hi
     moe_mv_shape(d->type, a.E, &li, &ni);
     moe_mv_shape(d->type, a.FE, &lo, &no);
     switch (d->type) {
-    case QT_Q8_0: return launch_fused_t<QT_Q8_0>(a, ni, lo, no, st);
-    case QT_ROCMFP4: return launch_fused_t<QT_ROCMFP4>(a, ni, lo, no, st);
-    default: return launch_fused_t<QT_ROCMFP4_FAST>(a, ni, lo, no, st);
+    case QT_Q8_0: return launch_fused_t<QT_Q8_0>(a, ni, lo, no, kernels, st);
+    case QT_ROCMFP4: return launch_fused_t<QT_ROCMFP4>(a, ni, lo, no, kernels, st);
+    default: return launch_fused_t<QT_ROCMFP4_FAST>(a, ni, lo, no, kernels, st);
     }
 }
 
@@ -325,7 +328,7 @@ static unsigned long long* g_stamps = nullptr;
 extern "C" void moe_layer_fused_stamps(void* stamps) { g_stamps = (unsigned long long*)stamps; }
 
 bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits, float* out, int* ids_out,
-                   float* wts_out, void* scratch, hipStream_t st, hipError_t* err) {
+                   float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err) {
     FArgs a = {};
     a.stamps = g_stamps;
     if (!moe_fused_prepare(d, a)) return false;
@@ -334,6 +337,6 @@ bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits,
     a.out = out;
     a.ids_out = ids_out;
     a.wts_out = wts_out;
-    *err = moe_fused_launch(d, a, scratch, st);
+    *err = moe_fused_launch(d, a, scratch, kernels, st);
     return true;
 }

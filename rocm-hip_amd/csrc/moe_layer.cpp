@@ -15,7 +15,7 @@ size_t moe_fused_scratch_bytes(const moe_layer_desc* d);
 
 // The fused decode kernel's arguments are built in fused_decode.hip; this file only sees these entry points
 bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits, float* out, int* ids_out,
-                   float* wts_out, void* scratch, hipStream_t st, hipError_t* err);
+                   float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err);
 
 static std::atomic<int> g_fused{1};
 
@@ -91,7 +91,9 @@ Plan plan(const moe_layer_desc* d, int T) {
 
 }  // namespace
 
-extern "C" void moe_layer_set_fused(int enable) { g_fused.store(enable ? 1 : 0); }
+extern "C" void moe_layer_set_fused(int mode) {
+    g_fused.store(mode == 0 || mode == 1 || (mode >= 0x100 && mode <= 0x107) ? mode : 1);
+}
 
 extern "C" size_t moe_layer_scratch_bytes(const moe_layer_desc* d, int max_t) {
     if (!d || max_t <= 0) return 0;
@@ -106,9 +108,11 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
     if (scratch_bytes < p.total) return hipErrorInvalidValue;
     const int E = d->n_embd, NE = d->n_expert, NU = d->n_used, FE = d->n_ff, type = d->type;
     const bool sh = d->s_gate != nullptr;
-    if (T == 1 && g_fused.load(std::memory_order_relaxed)) {
+    const int mode = g_fused.load(std::memory_order_relaxed);
+    if (T == 1 && mode) {
         hipError_t e = hipSuccess;
-        if (moe_fused_try(d, x, logits_in, out, ids_out, wts_out, scratch, st, &e)) return e;
+        const int kernels = mode == 1 ? 7 : mode & 7;
+        if (moe_fused_try(d, x, logits_in, out, ids_out, wts_out, scratch, kernels, st, &e)) return e;
     }
     const size_t rb_in = row_size(type, E), rb_out = row_size(type, FE);
     char* s = (char*)scratch;
