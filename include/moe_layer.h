@@ -53,7 +53,7 @@ void moe_layer_set_fused(int mode);
 
 // No counterpart in the reference (its QWEN_PROFILE times sections on the host). Profiling: every later fused
 // layer writes wall-clock stamps (100 MHz) per workgroup to stamps: [workgroup][8], kernel 1 in columns 0, 1
-// (start, done), kernel 2 in 2..4 (start, routed, done), kernel 3 in 5, 6; rows for the largest grid
+// (start, done), kernel 2 in 2..4 (start, routed, done) and 7 (row dots done), kernel 3 in 5, 6; rows for the largest grid
 // (max(NE + 2, NS * FE / 32, E) always suffices); NULL stops. Launches capture the pointer current at the call.
 void moe_layer_fused_stamps(void* stamps);
 

@@ -50,7 +50,7 @@ struct FArgs {
 };
 
 // Timestamp k of this workgroup (the 100 MHz wall clock), when stamps are requested: kernel 1 uses slots 0, 1,
-// kernel 2 slots 2..4, kernel 3 slots 5, 6 of row blockIdx.x of a [max grid][8] table
+// kernel 2 slots 2..4 and 7 (row dots done), kernel 3 slots 5, 6 of row blockIdx.x of a [max grid][8] table
 __device__ __forceinline__ void stamp(const FArgs& a, int k) {
     if (a.stamps && threadIdx.x == 0) a.stamps[blockIdx.x * 8 + k] = wall_clock64();
 }
@@ -158,6 +158,7 @@ __global__ void __launch_bounds__(64 * (64 / FD_GU_RW)) k_fd_gate_up(FArgs a) {
 #pragma unroll
         for (int r = 0; r < RW; ++r) gu[mat][RW * (w % WPM) + r] = acc[r];
     __syncthreads();
+    stamp(a, 7);
     if (w == 0) {  // SwiGLU (the swiglu kernel's expression) and the Q8_0 block of these 32 values
         const int t = lane & 31;
         const float g = gu[0][t], uu = gu[1][t];
