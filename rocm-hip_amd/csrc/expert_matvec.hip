@@ -480,15 +480,28 @@ extern "C" hipError_t qmatvec_launch_q8(int type, const void* W, size_t row_byte
     return dense(type, W, N, y, nullptr, 0, nullptr, row_bytes, q, K, 1, N, stream);
 }
 
+bool moe_grouped_mfma_ok(int type, int N, int K);
+hipError_t moe_launch_dense_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
+                                 const qmatvec_q8* q, float* y, long long ldy, int N, int K, int T,
+                                 hipStream_t stream);
+
+// From T = 8 tokens a registered matrix runs on the MFMA kernel (its weights read once for 64 tokens), below it
+// on the matvec kernel (weights once per token, from L2 after the first)
+#define DENSE_MFMA_MIN_T 8
+
 extern "C" hipError_t qmatvec_launch_q8_batch(int type, const void* W, size_t row_bytes, const qmatvec_q8* q, float* y,
                                               long long ldy, int N, int K, int T, hipStream_t stream) {
+    const uint8_t *v = nullptr, *s = nullptr;
+    if (T >= DENSE_MFMA_MIN_T && N > 0 && ldy >= N && y && check_common(type, W, row_bytes, q, K, T) == hipSuccess &&
+        moe_grouped_mfma_ok(type, N, K) && find_packed(W, type, K, row_bytes, &v, &s))
+        return moe_launch_dense_mfma(type, v, s, fmt_value_row(type, K), fmt_scale_row(type, K), q, y, ldy, N, K, T,
+                                     stream);
     return dense(type, W, N, y, nullptr, 0, nullptr, row_bytes, q, K, T, ldy, stream);
 }
 
 // Entry tiles of the grouped kernels (the MFMA kernel's 64; the per-entry fallback takes any)
 #define ENTRY_TILE 64
 
-bool moe_grouped_mfma_ok(int type, int N, int K);
 hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
                                    const qmatvec_q8* q, float* y, int N, int K, int max_tiles, const int32_t* n_tiles,
                                    const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,

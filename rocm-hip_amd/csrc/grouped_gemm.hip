@@ -35,8 +35,10 @@ struct GArgs {
     const int* tile_e;
     const int* tile_start;
     const int* tile_n;
-    const int* in_rows;
-    const int* out_rows;
+    const int* in_rows;   // nullptr: entry i of a tile is activation row tile_start + i
+    const int* out_rows;  // nullptr: entry i writes output row tile_start + i
+    long long ldy;        // output row stride
+    int T;                // n_tiles == nullptr (dense): T rows of one matrix in tiles of GG_TILE
 };
 
 #define GG_ROWS 128  // weight rows per workgroup (32 per wave)
@@ -158,10 +160,21 @@ template <int TYPE>
 __global__ void __launch_bounds__(256) k_grouped_mfma(GArgs a) {
     __shared__ __attribute__((aligned(1024))) GBuf buf;
     const int k = blockIdx.y;
-    if (k >= *a.n_tiles) return;
+    int e, st, cnt;
+    if (a.n_tiles) {
+        if (k >= *a.n_tiles) return;
+        e = a.tile_e[k];
+        st = a.tile_start[k];
+        cnt = __builtin_amdgcn_readfirstlane(a.tile_n[k]);
+    } else {  // dense: tile k is rows 64 k .. of the one matrix
+        st = k * GG_TILE;
+        if (st >= a.T) return;
+        e = 0;
+        cnt = min(GG_TILE, a.T - st);
+    }
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lr = l & 31, kh = l >> 5;
-    const int e = a.tile_e[k], st = a.tile_start[k];
-    const int cnt = __builtin_amdgcn_readfirstlane(a.tile_n[k]);
+    auto in_row = [&](int i) { return a.in_rows ? a.in_rows[st + i] : st + i; };
+    auto out_row = [&](int i) { return a.out_rows ? a.out_rows[st + i] : st + i; };
     const int K = a.K, nb = K / 32;
     // this lane's weight row (the launcher requires N % 128 == 0 and K % (32 GG_KB) == 0)
     const int r0 = blockIdx.x * GG_ROWS + 32 * w;
@@ -170,9 +183,9 @@ __global__ void __launch_bounds__(256) k_grouped_mfma(GArgs a) {
     const uint8_t* srow = a.s + grow * a.srb;
     // activation loads: this wave loads blocks (w >> 1) and (w >> 1) + 2 of tile (w & 1), entry 32 (w & 1) + lr
     const int tile_b = w & 1;
-    const int8_t* xrow = a.xq + (long long)a.in_rows[st + min(32 * tile_b + lr, cnt - 1)] * K + 16 * kh;
+    const int8_t* xrow = a.xq + (long long)in_row(min(32 * tile_b + lr, cnt - 1)) * K + 16 * kh;
     // activation scales: this wave's lanes 0..15 load entries 16 w + l
-    const float* dxr = a.xd + (long long)a.in_rows[st + min(16 * w + (l & 15), cnt - 1)] * nb;
+    const float* dxr = a.xd + (long long)in_row(min(16 * w + (l & 15), cnt - 1)) * nb;
 
     v16f acc0 = {}, acc1 = {};
     const int nst = nb / GG_KB;
@@ -188,12 +201,12 @@ __global__ void __launch_bounds__(256) k_grouped_mfma(GArgs a) {
     }
     // acc[j] is C[row 8 (j / 4) + 4 kh + j % 4][entry lr] of the wave's 32 x 32 tile
     if (lr < cnt) {
-        float* y = a.y + (long long)a.out_rows[st + lr] * a.N + r0;
+        float* y = a.y + (long long)out_row(lr) * a.ldy + r0;
 #pragma unroll
         for (int j = 0; j < 16; ++j) y[8 * (j >> 2) + 4 * kh + (j & 3)] = acc0[j];
     }
     if (32 + lr < cnt) {
-        float* y = a.y + (long long)a.out_rows[st + 32 + lr] * a.N + r0;
+        float* y = a.y + (long long)out_row(32 + lr) * a.ldy + r0;
 #pragma unroll
         for (int j = 0; j < 16; ++j) y[8 * (j >> 2) + 4 * kh + (j & 3)] = acc1[j];
     }
@@ -210,8 +223,22 @@ hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s,
                                    const qmatvec_q8* q, float* y, int N, int K, int max_tiles, const int32_t* n_tiles,
                                    const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
                                    const int32_t* in_rows, const int32_t* out_rows, hipStream_t stream) {
-    GArgs a = {v, s, vrb, srb, q->q0, q->d0, y, N, K, n_tiles, tile_e, tile_start, tile_n, in_rows, out_rows};
+    GArgs a = {v, s, vrb, srb, q->q0, q->d0, y, N, K, n_tiles, tile_e, tile_start, tile_n, in_rows, out_rows, N, 0};
     const dim3 g((N + GG_ROWS - 1) / GG_ROWS, max_tiles), b(256);
+    switch (type) {
+    case QT_Q8_0: return launch_kernel(k_grouped_mfma<QT_Q8_0>, g, b, 0, stream, a);
+    case QT_ROCMFP4: return launch_kernel(k_grouped_mfma<QT_ROCMFP4>, g, b, 0, stream, a);
+    case QT_ROCMFP4_FAST: return launch_kernel(k_grouped_mfma<QT_ROCMFP4_FAST>, g, b, 0, stream, a);
+    }
+    return hipErrorInvalidDeviceFunction;
+}
+
+// Dense: y[t][0..N) (row stride ldy) = W . x_t for t < T, every token a tile entry of the one matrix
+hipError_t moe_launch_dense_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
+                                 const qmatvec_q8* q, float* y, long long ldy, int N, int K, int T,
+                                 hipStream_t stream) {
+    GArgs a = {v, s, vrb, srb, q->q0, q->d0, y, N, K, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, ldy, T};
+    const dim3 g(N / GG_ROWS, (T + GG_TILE - 1) / GG_TILE), b(256);
     switch (type) {
     case QT_Q8_0: return launch_kernel(k_grouped_mfma<QT_Q8_0>, g, b, 0, stream, a);
     case QT_ROCMFP4: return launch_kernel(k_grouped_mfma<QT_ROCMFP4>, g, b, 0, stream, a);
