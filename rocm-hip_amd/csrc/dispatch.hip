@@ -6,112 +6,143 @@
 // reference orders entries inside an expert's run by atomic slot (nondeterministic); here they are in ascending
 // entry order, so the permutation is a pure function of ids.
 //
-// One workgroup of 16 waves. The permutation runs over chunks of 1024 tokens, one token per lane: each wave ORs
-// its lanes into a 64-bit mask per expert in LDS (bit l = lane l's token chose that expert); an entry's rank in
-// its expert's run is the running count from earlier chunks, plus the popcounts of the lower waves' masks, plus
-// the popcount of its own wave's mask below its lane. A token's repeated id (a malformed row) and ids outside
-// [0, n_expert) are skipped everywhere, so the counts, ranks and positions stay consistent.
+// One workgroup of 8 waves; tokens in chunks of 512, one token per lane. Per chunk each wave ORs its lanes into a
+// 64-bit mask per expert in LDS (bit l: lane l's token chose that expert); one thread per expert then turns the
+// masks into counts and into each wave's prefix (the entries of that expert in the chunk's lower waves). Pass 1
+// sums the counts over the chunks (then the scans and the tile table); pass 2 places each entry at its expert's
+// offset + the entries of earlier chunks + its wave's prefix + the popcount of its wave's mask below its lane.
+// A token's repeated id (a malformed row) and ids outside [0, n_expert) are skipped everywhere.
 
 #include "gpu_ops.h"
 #include "host_common.h"
 #include "moe_common.h"
 
-#define GROUP_WAVES 16
+#define GROUP_WAVES 8
+#define GROUP_MAX_NU 16  // ids of a token held in registers; wider rows read them from memory
 
-// Whether entry j of the token's row is the first occurrence of a valid expert id
-__device__ __forceinline__ bool group_valid(const int* row, int j, int ne) {
-    const int e = row[j];
-    if (e < 0 || e >= ne) return false;
-    for (int k = 0; k < j; ++k)
-        if (row[k] == e) return false;
-    return true;
+// Bit j: entry j of the token's row is the first occurrence of a valid expert id
+__device__ __forceinline__ uint64_t group_valid_mask(const int* row, int nu, int ne) {
+    uint64_t m = 0;
+    if (nu <= GROUP_MAX_NU) {
+        int r[GROUP_MAX_NU];
+#pragma unroll
+        for (int j = 0; j < GROUP_MAX_NU; ++j) r[j] = j < nu ? row[j] : -1;
+#pragma unroll
+        for (int j = 0; j < GROUP_MAX_NU; ++j) {
+            bool ok = j < nu && r[j] >= 0 && r[j] < ne;
+#pragma unroll
+            for (int k = 0; k < j; ++k) ok = ok && r[k] != r[j];
+            m |= (uint64_t)ok << j;
+        }
+    } else {
+        for (int j = 0; j < nu; ++j) {
+            const int e = row[j];
+            bool ok = e >= 0 && e < ne;
+            for (int k = 0; k < j && ok; ++k) ok = row[k] != e;
+            m |= (uint64_t)ok << j;
+        }
+    }
+    return m;
 }
 
-__global__ void __launch_bounds__(1024) k_moe_group(const int* ids, int T, int nu, int ne, int tile, int* tok_rows,
-                                                    int* pair_rows, int* n_tiles, int* tile_e, int* tile_start,
-                                                    int* tile_n) {
+__global__ void __launch_bounds__(64 * GROUP_WAVES) k_moe_group(const int* ids, int T, int nu, int ne, int tile,
+                                                                int* tok_rows, int* pair_rows, int* n_tiles,
+                                                                int* tile_e, int* tile_start, int* tile_n) {
     extern __shared__ unsigned long long g_smem[];
-    unsigned long long* masks = g_smem;                     // [GROUP_WAVES][ne]
-    int* cnt = (int*)(masks + (size_t)GROUP_WAVES * ne);    // [ne] entry counts
-    int* eoff = cnt + ne;                                   // [ne] first entry of each expert
-    int* run = eoff + ne;                                   // [ne] entries placed by earlier chunks
+    constexpr int NT = 64 * GROUP_WAVES;
+    unsigned long long* masks = g_smem;                            // [GROUP_WAVES][ne]
+    uint16_t* pre = (uint16_t*)(masks + (size_t)GROUP_WAVES * ne);  // [GROUP_WAVES][ne] wave prefixes
+    int* cnt = (int*)(pre + (size_t)GROUP_WAVES * ne);             // [ne] entry counts (16 ne bytes in)
+    int* eoff = cnt + ne;                                          // [ne] first entry of each expert
+    int* run = eoff + ne;                                          // [ne] entries of earlier chunks
     __shared__ int wpart[2][GROUP_WAVES];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-
-    for (int e = tid; e < ne; e += 1024) cnt[e] = run[e] = 0;
-    __syncthreads();
-    const int n = T * nu;
-    for (int i = tid; i < n; i += 1024) {
-        const int t = i / nu, j = i - t * nu;
-        if (group_valid(ids + (size_t)t * nu, j, ne)) atomicAdd(&cnt[ids[i]], 1);
-    }
-    __syncthreads();
-
-    // exclusive scans over the experts, one expert per thread (ne <= 1024)
-    const int c = tid < ne ? cnt[tid] : 0, nt = (c + tile - 1) / tile;
-    int a = c, b = nt;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int ua = __shfl_up(a, d, 64), ub = __shfl_up(b, d, 64);
-        if (lane >= d) {
-            a += ua;
-            b += ub;
-        }
-    }
-    if (lane == 63) {
-        wpart[0][w] = a;
-        wpart[1][w] = b;
-    }
-    __syncthreads();
-    int ba = 0, bb = 0;
-    for (int k = 0; k < w; ++k) {
-        ba += wpart[0][k];
-        bb += wpart[1][k];
-    }
-    const int eo = ba + a - c, to = bb + b - nt;
-    if (tid < ne) {
-        eoff[tid] = eo;
-        for (int k = 0; k < nt; ++k) {
-            tile_e[to + k] = tid;
-            tile_start[to + k] = eo + k * tile;
-            tile_n[to + k] = min(tile, c - k * tile);
-        }
-        if (tid == ne - 1) *n_tiles = to + nt;
-    }
-    __syncthreads();
-
     unsigned long long* my = masks + (size_t)w * ne;
     const unsigned long long below = (1ull << lane) - 1ull;
-    for (int t0 = 0; t0 < T; t0 += 1024) {
-        for (int e = lane; e < ne; e += 64) my[e] = 0ull;
-        __syncthreads();
-        const int t = t0 + tid;
-        const int* row = ids + (size_t)t * nu;
-        if (t < T)
+
+    for (int e = tid; e < ne; e += NT) cnt[e] = run[e] = 0;
+    // pass 0: counts; pass 1: placement
+    for (int pass = 0; pass < 2; ++pass) {
+        for (int t0 = 0; t0 < T; t0 += NT) {
+            for (int e = lane; e < ne; e += 64) my[e] = 0ull;
+            __syncthreads();
+            const int t = t0 + tid;
+            const int* row = ids + (size_t)t * nu;
+            const uint64_t vm = t < T ? group_valid_mask(row, nu, ne) : 0ull;
             for (int j = 0; j < nu; ++j)
-                if (group_valid(row, j, ne)) atomicOr(&my[row[j]], 1ull << lane);
-        __syncthreads();
-        if (t < T)
-            for (int j = 0; j < nu; ++j) {
-                if (!group_valid(row, j, ne)) continue;
-                const int e = row[j];
-                int r = run[e] + __popcll(my[e] & below);
-                for (int k = 0; k < w; ++k) r += __popcll(masks[(size_t)k * ne + e]);
-                const int p = eoff[e] + r;
-                tok_rows[p] = t;
-                pair_rows[p] = t * nu + j;
+                if ((vm >> j) & 1) atomicOr(&my[row[j]], 1ull << lane);
+            __syncthreads();
+            for (int e = tid; e < ne; e += NT) {  // prefixes over the waves, the chunk's count
+                int s = 0;
+#pragma unroll
+                for (int k = 0; k < GROUP_WAVES; ++k) {
+                    pre[(size_t)k * ne + e] = (uint16_t)s;
+                    s += __popcll(masks[(size_t)k * ne + e]);
+                }
+                if (pass == 0) cnt[e] += s;
             }
-        __syncthreads();
-        for (int e = tid; e < ne; e += 1024) {
-            int s = 0;
-            for (int k = 0; k < GROUP_WAVES; ++k) s += __popcll(masks[(size_t)k * ne + e]);
-            run[e] += s;
+            __syncthreads();
+            if (pass == 1) {
+                for (int j = 0; j < nu; ++j) {
+                    if (!((vm >> j) & 1)) continue;
+                    const int e = row[j];
+                    const int p = eoff[e] + run[e] + pre[(size_t)w * ne + e] + __popcll(my[e] & below);
+                    tok_rows[p] = t;
+                    pair_rows[p] = t * nu + j;
+                }
+                __syncthreads();
+                for (int e = tid; e < ne; e += NT)
+                    run[e] += pre[(size_t)(GROUP_WAVES - 1) * ne + e] + __popcll(masks[(size_t)(GROUP_WAVES - 1) * ne + e]);
+            }
+            __syncthreads();
         }
-        __syncthreads();
+        if (pass == 1) break;
+        // exclusive scans over the experts (entries and tiles), one expert per thread and round
+        int ca = 0, cb = 0;  // carries of earlier rounds
+        for (int e0 = 0; e0 < ne; e0 += NT) {
+            const int e = e0 + tid;
+            const int c = e < ne ? cnt[e] : 0, nt = (c + tile - 1) / tile;
+            int a = c, b = nt;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int ua = __shfl_up(a, d, 64), ub = __shfl_up(b, d, 64);
+                if (lane >= d) {
+                    a += ua;
+                    b += ub;
+                }
+            }
+            if (lane == 63) {
+                wpart[0][w] = a;
+                wpart[1][w] = b;
+            }
+            __syncthreads();
+            int ba = ca, bb = cb;
+            for (int k = 0; k < w; ++k) {
+                ba += wpart[0][k];
+                bb += wpart[1][k];
+            }
+            const int eo = ba + a - c, to = bb + b - nt;
+            if (e < ne) {
+                eoff[e] = eo;
+                for (int k = 0; k < nt; ++k) {
+                    tile_e[to + k] = e;
+                    tile_start[to + k] = eo + k * tile;
+                    tile_n[to + k] = min(tile, c - k * tile);
+                }
+                if (e == ne - 1) *n_tiles = to + nt;
+            }
+            for (int k = 0; k < GROUP_WAVES; ++k) {
+                ca += wpart[0][k];
+                cb += wpart[1][k];
+            }
+            __syncthreads();
+        }
     }
 }
 
-static size_t group_smem(int ne) { return (size_t)GROUP_WAVES * ne * 8 + 3 * (size_t)ne * 4; }
+static size_t group_smem(int ne) {
+    return (size_t)GROUP_WAVES * ne * 8 + (size_t)GROUP_WAVES * ne * 2 + 4 + 3 * (size_t)ne * 4;
+}
 
 extern "C" hipError_t gpu_moe_group(const int* ids, int T, int n_used, int n_expert, int tile, int* tok_rows,
                                     int* pair_rows, int* n_tiles, int* tile_e, int* tile_start, int* tile_n,
@@ -128,6 +159,6 @@ extern "C" hipError_t gpu_moe_group(const int* ids, int T, int n_used, int n_exp
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    return launch_kernel(k_moe_group, dim3(1), dim3(1024), shm, stream, ids, T, n_used, n_expert, tile, tok_rows,
+    return launch_kernel(k_moe_group, dim3(1), dim3(64 * GROUP_WAVES), shm, stream, ids, T, n_used, n_expert, tile, tok_rows,
                          pair_rows, n_tiles, tile_e, tile_start, tile_n);
 }
