@@ -7,9 +7,9 @@
 //           experts' width and type), SwiGLU quantized for down, down, moe_combine;
 //   T 2..7: the same per token (each token's experts read once per token);
 //   T >= 8: gpu_moe_group, the grouped gate / up / down on the expert tiles, the shared expert dense, combine.
-// T == 1 with every expert matrix registered (qmatvec_pack_weights) runs as three fused kernels with the same
-// results bit for bit. All buffers are device memory; scratch is caller-owned (moe_layer_scratch_bytes).
-// Asynchronous on `stream`.
+// T <= 7 with every expert matrix registered (qmatvec_pack_weights) runs as three fused kernels with the same
+// results bit for bit (T >= 2: each distinct expert's rows read once for all the tokens that chose it). All
+// buffers are device memory; scratch is caller-owned (moe_layer_scratch_bytes). Asynchronous on `stream`.
 
 #ifndef MOE_LAYER_H
 #define MOE_LAYER_H

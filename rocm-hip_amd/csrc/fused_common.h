@@ -1,0 +1,123 @@
+// fused_common.h -- device pieces shared by the fused decode-layer kernels (fused_decode.hip: one token;
+// fused_multi.hip: 2..7 tokens). Each restates a per-operation kernel's expressions, so the fused layers produce
+// the per-operation path's bits.
+#ifndef FUSED_COMMON_H
+#define FUSED_COMMON_H
+
+#include "expert_units.h"
+#include "moe_layer.h"
+#include "router_dev.h"
+
+#define FD_MAX_E 4096  // largest E the fused kernels take
+#define FD_MAX_T 7     // largest token count of the multi-token fused kernels (T >= 8 is the grouped path)
+
+// Arguments of the fused kernels (T = 1: fused_decode.hip; T = 2..FD_MAX_T: fused_multi.hip)
+struct FArgs {
+    const float* x;          // [T][E]
+    const float* logits_in;  // [T][NE] or nullptr
+    const float* w_router;   // [NE][E]
+    const float* w_shexp;    // [E] or nullptr
+    const uint8_t* v[6];     // value planes: gate, up, down (stacked experts), shared gate, up, down
+    const uint8_t* s[6];     // scale planes
+    long long vrb_in, srb_in, vrb_out, srb_out;  // plane row bytes for K = E and K = FE
+    float* out;              // [T][E]
+    int* ids_out;            // [T][NU] or nullptr
+    float* wts_out;          // [T][NU] or nullptr
+    float* logits;           // scratch [T][NE]
+    float* sg;               // scratch [T]
+    int8_t* xq;              // scratch: x quantized, Q8_0 values [T][E] and scales [T][E / 32]
+    float* xd;
+    int* ids;                // scratch: the routing [T][NU]
+    float* wts;
+    int8_t* act_q;           // scratch [T][NS][FE]
+    float* act_d;            // scratch [T][NS][FE / 32]
+    unsigned long long* stamps;  // optional timestamps (profiling, one token): [workgroup][8], nullptr: none
+    int T, E, NE, NU, FE, NS, has_gate;
+};
+
+// Timestamp k of this workgroup (the 100 MHz wall clock), when stamps are requested: kernel 1 uses slots 0, 1,
+// kernel 2 slots 2..4 and 7, kernel 3 slots 5, 6 of row blockIdx.x of a [max grid][8] table
+__device__ __forceinline__ void stamp(const FArgs& a, int k) {
+    if (a.stamps && threadIdx.x == 0) a.stamps[blockIdx.x * 8 + k] = wall_clock64();
+}
+
+// Host side, fused_decode.hip: whether the fused kernels take this layer (type, shapes, every expert matrix
+// registered) with the planes and row bytes filled in; the scratch bytes of T tokens and its carve-up; the lane
+// shapes (gate / up K = E: lanes li, units ni; down K = FE: lo, no)
+bool moe_fused_prepare(const moe_layer_desc* d, FArgs& a);
+size_t moe_fused_scratch_bytes(const moe_layer_desc* d, int T);
+void moe_fused_carve(FArgs& a, void* scratch);
+void moe_mv_shape(int type, int K, int* lanes, int* units_per_lane);
+unsigned long long* moe_fused_stamps_ptr();  // the table moe_layer_fused_stamps set, or nullptr
+
+// Row dots of R rows per lane group of L lanes, each with its own weight row and input row (split-plane weights):
+// all loads first, then the units in ascending order per row (rows_dot's order), then the group sums. Only rows
+// r < nvalid are loaded; the others' results are undefined.
+template <int TYPE, int L, int R, int NUPL>
+__device__ __forceinline__ void rows_dot_multi(const uint8_t* const vr[R], const uint8_t* const sr[R],
+                                               const int8_t* const xq[R], const float* const xd[R], int nu, int gl,
+                                               int nvalid, float acc[R]) {
+    WUnit<TYPE> w[R][NUPL];
+    XUnit<TYPE> x[R][NUPL];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        if (r < nvalid)
+#pragma unroll
+            for (int i = 0; i < NUPL; ++i) load_packed<TYPE>(vr[r], sr[r], gl + i * L, nu, w[r][i]);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        if (r < nvalid)
+#pragma unroll
+            for (int i = 0; i < NUPL; ++i) load_x<TYPE>(xq[r], xd[r], nullptr, gl + i * L, x[r][i]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        acc[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NUPL; ++i) acc[r] += term<TYPE>(w[r][i], x[r][i], gl + i * L);
+        acc[r] = group_sum<L>(acc[r]);
+    }
+}
+
+// Q8_0 of one row of E values by a 256-thread workgroup, 8 values per thread (4 threads per block of 32): the
+// activation quantizer's expressions (amax, id = 127 / amax, rint, d = F16(amax / 127))
+__device__ __forceinline__ void quantize_row_q8_0(const float* x, int E, int8_t* xq, float* xd) {
+    const int tid = threadIdx.x;
+    for (int base = 0; base < E; base += 2048) {
+        const int i0 = base + 8 * tid;
+        float v[8];
+        float am = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v[j] = i0 + j < E ? x[i0 + j] : 0.0f;
+            am = fmaxf(am, fabsf(v[j]));
+        }
+        am = group_max<4>(am);
+        const float id = am != 0.0f ? 127.0f / am : 0.0f;
+        if (i0 < E) {
+            int q[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) q[j] = (int)rintf(v[j] * id);
+            *(uint2*)(xq + i0) = make_uint2((q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) |
+                                                ((uint32_t)q[3] << 24),
+                                            (q[4] & 0xff) | ((q[5] & 0xff) << 8) | ((q[6] & 0xff) << 16) |
+                                                ((uint32_t)q[7] << 24));
+            if ((tid & 3) == 0) xd[i0 / 32] = __half2float(__float2half(am / 127.0f));
+        }
+    }
+}
+
+// One wave: SwiGLU of 32 gate / up values (the swiglu kernel's expression) and their Q8_0 block; lanes 0..31 write
+// the 32 codes to q[0..32), lane 0 the scale to *d
+__device__ __forceinline__ void swiglu_q8_block(const float* g32, const float* u32, int8_t* q, float* d) {
+    const int lane = threadIdx.x & 63, t = lane & 31;
+    const float g = g32[t], uu = u32[t];
+    const float act = g / (1.0f + __expf(-g)) * uu;
+    const float am = group_max<32>(fabsf(act));
+    const float id = am != 0.0f ? 127.0f / am : 0.0f;
+    if (lane < 32) {
+        q[t] = (int8_t)(int)rintf(act * id);
+        if (t == 0) *d = __half2float(__float2half(am / 127.0f));
+    }
+}
+
+#endif  // FUSED_COMMON_H

@@ -15,73 +15,16 @@
 // (A single persistent kernel with two grid barriers was measured slower: each barrier's cross-XCD fences and
 // 256-way atomic arrival cost ~10 us on MI355X, more than a kernel boundary.)
 
-#include "expert_units.h"
+#include "fused_common.h"
 #include "host_common.h"
 #include "moe_layer.h"
 #include "qmatvec.h"
-#include "router_dev.h"
 
-#define FD_MAX_E 4096
 #ifndef FD_GU_RW
 #define FD_GU_RW 4              // gate / up rows per wave in kernel 2 (64 / FD_GU_RW waves per workgroup)
 #endif
 
-struct FArgs {
-    const float* x;          // [E]
-    const float* logits_in;  // [NE] or nullptr
-    const float* w_router;   // [NE][E]
-    const float* w_shexp;    // [E] or nullptr
-    const uint8_t* v[6];     // value planes: gate, up, down (stacked experts), shared gate, up, down
-    const uint8_t* s[6];     // scale planes
-    long long vrb_in, srb_in, vrb_out, srb_out;  // plane row bytes for K = E and K = FE
-    float* out;              // [E]
-    int* ids_out;            // [NU] or nullptr
-    float* wts_out;          // [NU] or nullptr
-    float* logits;           // scratch [NE]
-    float* sg;               // scratch [1]
-    int8_t* xq;              // scratch: x quantized, Q8_0 values [E] and scales [E / 32]
-    float* xd;
-    int* ids;                // scratch: the routing [NU]
-    float* wts;
-    int8_t* act_q;           // scratch [NS][FE]
-    float* act_d;            // scratch [NS][FE / 32]
-    unsigned long long* stamps;  // optional timestamps (profiling): [kernel 1 | 2 | 3 workgroups][6], nullptr: none
-    int E, NE, NU, FE, NS, has_gate;
-};
 
-// Timestamp k of this workgroup (the 100 MHz wall clock), when stamps are requested: kernel 1 uses slots 0, 1,
-// kernel 2 slots 2..4 and 7 (row dots done), kernel 3 slots 5, 6 of row blockIdx.x of a [max grid][8] table
-__device__ __forceinline__ void stamp(const FArgs& a, int k) {
-    if (a.stamps && threadIdx.x == 0) a.stamps[blockIdx.x * 8 + k] = wall_clock64();
-}
-
-// The down phase's row dots: R row dots per lane group of L lanes, each with its own weight row and input row;
-// all loads first, then the units in ascending order per row (rows_dot's order), then the group sums
-// (only rows r < nvalid are loaded; the others' results are undefined)
-template <int TYPE, int L, int R, int NUPL>
-__device__ __forceinline__ void rows_dot_multi(const uint8_t* const vr[R], const uint8_t* const sr[R],
-                                               const int8_t* const xq[R], const float* const xd[R], int nu, int gl,
-                                               int nvalid, float acc[R]) {
-    WUnit<TYPE> w[R][NUPL];
-    XUnit<TYPE> x[R][NUPL];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-        if (r < nvalid)
-#pragma unroll
-            for (int i = 0; i < NUPL; ++i) load_packed<TYPE>(vr[r], sr[r], gl + i * L, nu, w[r][i]);
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-        if (r < nvalid)
-#pragma unroll
-            for (int i = 0; i < NUPL; ++i) load_x<TYPE>(xq[r], xd[r], nullptr, gl + i * L, x[r][i]);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        acc[r] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NUPL; ++i) acc[r] += term<TYPE>(w[r][i], x[r][i], gl + i * L);
-        acc[r] = group_sum<L>(acc[r]);
-    }
-}
 
 // ---- kernel 1: router logits (workgroups 0 .. NE - 1), x quantized (workgroup NE), the shared gate (NE + 1)
 __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
@@ -100,29 +43,7 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
         stamp(a, 1);
         return;
     }
-    // Q8_0 per 32 values (4 threads of 8 values): the quantizer's expressions
-    for (int base = 0; base < E; base += 2048) {
-        const int i0 = base + 8 * tid;
-        float v[8];
-        float am = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            v[j] = i0 + j < E ? a.x[i0 + j] : 0.0f;
-            am = fmaxf(am, fabsf(v[j]));
-        }
-        am = group_max<4>(am);
-        const float id = am != 0.0f ? 127.0f / am : 0.0f;
-        if (i0 < E) {
-            int q[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) q[j] = (int)rintf(v[j] * id);
-            *(uint2*)(a.xq + i0) = make_uint2((q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) |
-                                                  ((uint32_t)q[3] << 24),
-                                              (q[4] & 0xff) | ((q[5] & 0xff) << 8) | ((q[6] & 0xff) << 16) |
-                                                  ((uint32_t)q[7] << 24));
-            if ((tid & 3) == 0) a.xd[i0 / 32] = __half2float(__float2half(am / 127.0f));
-        }
-    }
+    quantize_row_q8_0(a.x, E, a.xq, a.xd);  // x quantized for gate / up
     stamp(a, 1);
 }
 
@@ -159,17 +80,8 @@ __global__ void __launch_bounds__(64 * (64 / FD_GU_RW)) k_fd_gate_up(FArgs a) {
         for (int r = 0; r < RW; ++r) gu[mat][RW * (w % WPM) + r] = acc[r];
     __syncthreads();
     stamp(a, 7);
-    if (w == 0) {  // SwiGLU (the swiglu kernel's expression) and the Q8_0 block of these 32 values
-        const int t = lane & 31;
-        const float g = gu[0][t], uu = gu[1][t];
-        const float act = g / (1.0f + __expf(-g)) * uu;
-        const float am = group_max<32>(fabsf(act));
-        const float id = am != 0.0f ? 127.0f / am : 0.0f;
-        if (lane < 32) {
-            a.act_q[(long long)slot * FE + 32 * b + t] = (int8_t)(int)rintf(act * id);
-            if (t == 0) a.act_d[(long long)slot * nbf + b] = __half2float(__float2half(am / 127.0f));
-        }
-    }
+    if (w == 0)  // SwiGLU and the Q8_0 block of these 32 values
+        swiglu_q8_block(gu[0], gu[1], a.act_q + (long long)slot * FE + 32 * b, a.act_d + (long long)slot * nbf + b);
     stamp(a, 4);
 }
 
@@ -208,7 +120,6 @@ __global__ void __launch_bounds__(1024) k_fd_down(FArgs a) {
 // ------------------------------------------------------------------ host side
 
 bool moe_packed_planes(const void* W, int type, int K, size_t row_bytes, const uint8_t** v, const uint8_t** s);
-void moe_mv_shape(int type, int K, int* lanes, int* units_per_lane);
 
 namespace {
 
@@ -248,12 +159,32 @@ namespace {
 size_t fa256(size_t v) { return (v + 255) & ~(size_t)255; }
 }
 
-// Scratch bytes of the three kernels: logits, gate, quantized x, routing, the quantized down input
-size_t moe_fused_scratch_bytes(const moe_layer_desc* d) {
-    const int NS = d->n_used + (d->s_gate ? 1 : 0);
-    const size_t E = d->n_embd;
-    return fa256((size_t)d->n_expert * 4) + fa256(4) + fa256(E) + fa256(E / 32 * 4) + 2 * fa256(64 * 4) +
-           fa256((size_t)NS * d->n_ff) + fa256((size_t)NS * d->n_ff / 32 * 4);
+// Scratch bytes of the three kernels for T tokens: logits, gates, quantized x, routing, the quantized down input
+size_t moe_fused_scratch_bytes(const moe_layer_desc* d, int T) {
+    const size_t NS = d->n_used + (d->s_gate ? 1 : 0), E = d->n_embd, t = T;
+    return fa256(t * d->n_expert * 4) + fa256(t * 4) + fa256(t * E) + fa256(t * E / 32 * 4) + 2 * fa256(t * 64 * 4) +
+           fa256(t * NS * d->n_ff) + fa256(t * NS * d->n_ff / 32 * 4);
+}
+
+// The scratch pieces of a.T tokens (the layout moe_fused_scratch_bytes sizes)
+void moe_fused_carve(FArgs& a, void* scratch) {
+    char* p = (char*)scratch;
+    const size_t t = a.T;
+    a.logits = (float*)p;
+    p += fa256(t * a.NE * 4);
+    a.sg = (float*)p;
+    p += fa256(t * 4);
+    a.xq = (int8_t*)p;
+    p += fa256(t * a.E);
+    a.xd = (float*)p;
+    p += fa256(t * a.E / 32 * 4);
+    a.ids = (int*)p;
+    p += fa256(t * 64 * 4);
+    a.wts = (float*)p;
+    p += fa256(t * 64 * 4);
+    a.act_q = (int8_t*)p;
+    p += fa256(t * a.NS * a.FE);
+    a.act_d = (float*)p;
 }
 
 // Whether the fused kernel takes this layer at T = 1: a Q8_0-activation type, every expert matrix registered in
@@ -296,22 +227,8 @@ bool moe_fused_prepare(const moe_layer_desc* d, FArgs& a) {
 }
 
 hipError_t moe_fused_launch(const moe_layer_desc* d, FArgs& a, void* scratch, int kernels, hipStream_t st) {
-    char* p = (char*)scratch;
-    a.logits = (float*)p;
-    p += fa256((size_t)a.NE * 4);
-    a.sg = (float*)p;
-    p += fa256(4);
-    a.xq = (int8_t*)p;
-    p += fa256((size_t)a.E);
-    a.xd = (float*)p;
-    p += fa256((size_t)a.E / 32 * 4);
-    a.ids = (int*)p;
-    p += fa256(64 * 4);
-    a.wts = (float*)p;
-    p += fa256(64 * 4);
-    a.act_q = (int8_t*)p;
-    p += fa256((size_t)a.NS * a.FE);
-    a.act_d = (float*)p;
+    a.T = 1;
+    moe_fused_carve(a, scratch);
     int li, ni, lo, no;
     moe_mv_shape(d->type, a.E, &li, &ni);
     moe_mv_shape(d->type, a.FE, &lo, &no);
@@ -327,6 +244,7 @@ static unsigned long long* g_stamps = nullptr;
 // Profiling: every later fused layer writes timestamps to stamps (device memory of 8 words per workgroup of the
 // largest of the three grids; nullptr: stop)
 extern "C" void moe_layer_fused_stamps(void* stamps) { g_stamps = (unsigned long long*)stamps; }
+unsigned long long* moe_fused_stamps_ptr() { return g_stamps; }
 
 bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits, float* out, int* ids_out,
                    float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err) {

@@ -212,6 +212,159 @@ __global__ void __launch_bounds__(256) k_grouped_mfma(GArgs a) {
     }
 }
 
+// ---- Register pipeline (no LDS, no barriers). Every wave loads its own MFMA operands straight from memory
+// into the operand registers: lane l holds weight row l % 32 / entry l % 32 and K half l / 32, which is exactly
+// one 16-byte half of a Q8_0 block (the split plane keeps the two halves of a row's blocks in two runs), 8 bytes
+// of a ROCmFP4 block's nibbles, or a FAST block's 16 bytes. The 4 waves of a workgroup share the activation
+// lines through L1. Stage s + 1's loads are issued before stage s's MFMAs, and several waves per SIMD hide the
+// rest of the latency.
+template <int TYPE, int KB>
+struct GStage {
+    uint4 a[KB];          // weights: Q8_0 / FAST 16 bytes; ROCmFP4 8 bytes in .x, .y
+    uint4 b0[KB], b1[KB];  // entries 0..31 / 32..63: Q8_0 / FAST 16 bytes; ROCmFP4 halves 0 (.x .y), 1 (.z .w)
+    float dx0[KB], dx1[KB];
+    uint2 ws;             // weight scales of the KB blocks (2 bytes per block; FAST 1 byte per block in .x)
+};
+
+template <int TYPE, int KB>
+__device__ __forceinline__ void gd_load(GStage<TYPE, KB>& S, int b0, const uint8_t* vrow, const uint8_t* srow,
+                                        const int8_t* x0, const int8_t* x1, const float* d0, const float* d1, int nb,
+                                        int kh) {
+#pragma unroll
+    for (int bb = 0; bb < KB; ++bb) {
+        const int b = b0 + bb;
+        if constexpr (TYPE == QT_Q8_0) {
+            S.a[bb] = *(const uint4*)(vrow + 16 * (kh ? nb + b : b));
+        } else if constexpr (TYPE == QT_ROCMFP4_FAST) {
+            S.a[bb] = *(const uint4*)(vrow + 16 * b);
+        } else {
+            const uint2 q = *(const uint2*)(vrow + 16 * b + 8 * kh);
+            S.a[bb] = make_uint4(q.x, q.y, 0u, 0u);
+        }
+        if constexpr (TYPE == QT_ROCMFP4) {
+            const uint2 p0 = *(const uint2*)(x0 + 32 * b + 8 * kh), q0 = *(const uint2*)(x0 + 32 * b + 16 + 8 * kh);
+            const uint2 p1 = *(const uint2*)(x1 + 32 * b + 8 * kh), q1 = *(const uint2*)(x1 + 32 * b + 16 + 8 * kh);
+            S.b0[bb] = make_uint4(p0.x, p0.y, q0.x, q0.y);
+            S.b1[bb] = make_uint4(p1.x, p1.y, q1.x, q1.y);
+        } else {
+            S.b0[bb] = *(const uint4*)(x0 + 32 * b + 16 * kh);
+            S.b1[bb] = *(const uint4*)(x1 + 32 * b + 16 * kh);
+        }
+        S.dx0[bb] = d0[b];
+        S.dx1[bb] = d1[b];
+    }
+    if constexpr (TYPE == QT_ROCMFP4_FAST) {
+        S.ws = make_uint2(KB == 4 ? *(const uint32_t*)(srow + b0) : (uint32_t) * (const uint16_t*)(srow + b0), 0u);
+    } else {
+        S.ws = KB == 4 ? *(const uint2*)(srow + 2 * b0) : make_uint2(*(const uint32_t*)(srow + 2 * b0), 0u);
+    }
+}
+
+template <int TYPE, int KB>
+__device__ __forceinline__ void gd_compute(const GStage<TYPE, KB>& S, v16f& acc0, v16f& acc1, int kh) {
+    const v16i zi = {};
+#pragma unroll
+    for (int bb = 0; bb < KB; ++bb) {
+        if constexpr (TYPE == QT_ROCMFP4) {
+            const uint32_t ew = (bb < 2 ? S.ws.x : S.ws.y) >> (16 * (bb & 1));
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t sh = 4 * h;
+                const long A = (long)(((unsigned long)fp4x4_to_i8x4(S.a[bb].y >> sh) << 32) |
+                                      fp4x4_to_i8x4(S.a[bb].x >> sh));
+                const float ee = ue4m3_half((ew >> (8 * h)) & 0xffu);
+                const long B0 = h ? (long)(((unsigned long)S.b0[bb].w << 32) | S.b0[bb].z)
+                                  : (long)(((unsigned long)S.b0[bb].y << 32) | S.b0[bb].x);
+                const long B1 = h ? (long)(((unsigned long)S.b1[bb].w << 32) | S.b1[bb].z)
+                                  : (long)(((unsigned long)S.b1[bb].y << 32) | S.b1[bb].x);
+                acc_block(acc0, __builtin_amdgcn_mfma_i32_32x32x16_i8(A, B0, zi, 0, 0, 0),
+                          scale_outer(ee, S.dx0[bb], kh));
+                acc_block(acc1, __builtin_amdgcn_mfma_i32_32x32x16_i8(A, B1, zi, 0, 0, 0),
+                          scale_outer(ee, S.dx1[bb], kh));
+            }
+        } else {
+            const uint4 q = S.a[bb];
+            v4i A;
+            float dw;
+            if constexpr (TYPE == QT_Q8_0) {
+                A = (v4i){(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+                dw = h2f((uint16_t)((bb < 2 ? S.ws.x : S.ws.y) >> (16 * (bb & 1))));
+            } else {
+                const uint32_t sh = kh ? 4 : 0;
+                A = (v4i){(int)fp4x4_to_i8x4(q.x >> sh), (int)fp4x4_to_i8x4(q.y >> sh), (int)fp4x4_to_i8x4(q.z >> sh),
+                          (int)fp4x4_to_i8x4(q.w >> sh)};
+                dw = ue4m3_half((S.ws.x >> (8 * bb)) & 0xffu);
+            }
+            const v4i B0 = {(int)S.b0[bb].x, (int)S.b0[bb].y, (int)S.b0[bb].z, (int)S.b0[bb].w};
+            const v4i B1 = {(int)S.b1[bb].x, (int)S.b1[bb].y, (int)S.b1[bb].z, (int)S.b1[bb].w};
+            acc_block(acc0, __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B0, zi, 0, 0, 0), scale_outer(dw, S.dx0[bb], kh));
+            acc_block(acc1, __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B1, zi, 0, 0, 0), scale_outer(dw, S.dx1[bb], kh));
+        }
+    }
+}
+
+template <int TYPE, int KB>
+__global__ void __launch_bounds__(256) k_grouped_direct(GArgs a) {
+    const int k = blockIdx.y;
+    int e, st, cnt;
+    if (a.n_tiles) {
+        if (k >= *a.n_tiles) return;
+        e = a.tile_e[k];
+        st = a.tile_start[k];
+        cnt = __builtin_amdgcn_readfirstlane(a.tile_n[k]);
+    } else {
+        st = k * GG_TILE;
+        if (st >= a.T) return;
+        e = 0;
+        cnt = min(GG_TILE, a.T - st);
+    }
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lr = l & 31, kh = l >> 5;
+    auto in_row = [&](int i) { return a.in_rows ? a.in_rows[st + i] : st + i; };
+    auto out_row = [&](int i) { return a.out_rows ? a.out_rows[st + i] : st + i; };
+    const int K = a.K, nb = K / 32;
+    const int r0 = blockIdx.x * GG_ROWS + 32 * w;
+    const long long grow = (long long)e * a.N + r0 + lr;
+    const uint8_t* vrow = a.v + grow * a.vrb;
+    const uint8_t* srow = a.s + grow * a.srb;
+    const long long i0 = in_row(min(lr, cnt - 1)), i1 = in_row(min(32 + lr, cnt - 1));
+    const int8_t* x0 = a.xq + i0 * K;
+    const int8_t* x1 = a.xq + i1 * K;
+    const float* d0 = a.xd + i0 * nb;
+    const float* d1 = a.xd + i1 * nb;
+
+    v16f acc0 = {}, acc1 = {};
+    const int nst = nb / KB;
+    GStage<TYPE, KB> cur, nxt;
+    gd_load<TYPE, KB>(cur, 0, vrow, srow, x0, x1, d0, d1, nb, kh);
+    for (int s = 0; s < nst; ++s) {
+        if (s + 1 < nst) gd_load<TYPE, KB>(nxt, (s + 1) * KB, vrow, srow, x0, x1, d0, d1, nb, kh);
+        gd_compute<TYPE, KB>(cur, acc0, acc1, kh);
+        cur = nxt;
+    }
+    if (lr < cnt) {
+        float* y = a.y + (long long)out_row(lr) * a.ldy + r0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) y[8 * (j >> 2) + 4 * kh + (j & 3)] = acc0[j];
+    }
+    if (32 + lr < cnt) {
+        float* y = a.y + (long long)out_row(32 + lr) * a.ldy + r0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) y[8 * (j >> 2) + 4 * kh + (j & 3)] = acc1[j];
+    }
+}
+
+#ifndef GG_DIRECT_KB
+#define GG_DIRECT_KB 0  // blocks per register stage of the direct kernel (0: the LDS pipeline)
+#endif
+
+template <int TYPE>
+static hipError_t launch_grouped_t(const GArgs& a, dim3 g, hipStream_t stream) {
+    if constexpr (GG_DIRECT_KB > 0)
+        return launch_kernel(k_grouped_direct<TYPE, GG_DIRECT_KB>, g, dim3(256), 0, stream, a);
+    else
+        return launch_kernel(k_grouped_mfma<TYPE>, g, dim3(256), 0, stream, a);
+}
+
 // Whether the MFMA kernel takes this matrix: a split-plane type with Q8_0 activations, whole 128-row blocks and
 // whole 4-block K stages
 bool moe_grouped_mfma_ok(int type, int N, int K) {
@@ -225,10 +378,11 @@ hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s,
                                    const int32_t* in_rows, const int32_t* out_rows, hipStream_t stream) {
     GArgs a = {v, s, vrb, srb, q->q0, q->d0, y, N, K, n_tiles, tile_e, tile_start, tile_n, in_rows, out_rows, N, 0};
     const dim3 g((N + GG_ROWS - 1) / GG_ROWS, max_tiles), b(256);
+    (void)b;
     switch (type) {
-    case QT_Q8_0: return launch_kernel(k_grouped_mfma<QT_Q8_0>, g, b, 0, stream, a);
-    case QT_ROCMFP4: return launch_kernel(k_grouped_mfma<QT_ROCMFP4>, g, b, 0, stream, a);
-    case QT_ROCMFP4_FAST: return launch_kernel(k_grouped_mfma<QT_ROCMFP4_FAST>, g, b, 0, stream, a);
+    case QT_Q8_0: return launch_grouped_t<QT_Q8_0>(a, g, stream);
+    case QT_ROCMFP4: return launch_grouped_t<QT_ROCMFP4>(a, g, stream);
+    case QT_ROCMFP4_FAST: return launch_grouped_t<QT_ROCMFP4_FAST>(a, g, stream);
     }
     return hipErrorInvalidDeviceFunction;
 }
@@ -239,10 +393,11 @@ hipError_t moe_launch_dense_mfma(int type, const uint8_t* v, const uint8_t* s, l
                                  hipStream_t stream) {
     GArgs a = {v, s, vrb, srb, q->q0, q->d0, y, N, K, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, ldy, T};
     const dim3 g(N / GG_ROWS, (T + GG_TILE - 1) / GG_TILE), b(256);
+    (void)b;
     switch (type) {
-    case QT_Q8_0: return launch_kernel(k_grouped_mfma<QT_Q8_0>, g, b, 0, stream, a);
-    case QT_ROCMFP4: return launch_kernel(k_grouped_mfma<QT_ROCMFP4>, g, b, 0, stream, a);
-    case QT_ROCMFP4_FAST: return launch_kernel(k_grouped_mfma<QT_ROCMFP4_FAST>, g, b, 0, stream, a);
+    case QT_Q8_0: return launch_grouped_t<QT_Q8_0>(a, g, stream);
+    case QT_ROCMFP4: return launch_grouped_t<QT_ROCMFP4>(a, g, stream);
+    case QT_ROCMFP4_FAST: return launch_grouped_t<QT_ROCMFP4_FAST>(a, g, stream);
     }
     return hipErrorInvalidDeviceFunction;
 }

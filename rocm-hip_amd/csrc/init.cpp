@@ -14,6 +14,10 @@
 #include "qmatvec.h"
 
 static std::atomic<int> g_ready{0};
+static std::atomic<int> g_cus{256};
+
+// Compute units of the initialised device (persistent grids size themselves by it)
+int moe_device_cus(void) { return g_cus.load(std::memory_order_relaxed); }
 
 extern "C" int moe_lib_ready(void) { return g_ready.load(std::memory_order_acquire); }
 
@@ -26,6 +30,7 @@ static int init_device(void) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return -1;
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return -1;
+    if (prop.multiProcessorCount > 0) g_cus.store(prop.multiProcessorCount, std::memory_order_relaxed);
     g_ready.store(1, std::memory_order_release);
     return 0;
 }

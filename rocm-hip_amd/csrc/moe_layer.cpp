@@ -11,13 +11,17 @@
 #include "qmatvec.h"
 
 struct FArgs;
-size_t moe_fused_scratch_bytes(const moe_layer_desc* d);
+size_t moe_fused_scratch_bytes(const moe_layer_desc* d, int T);
 
 // The fused decode kernel's arguments are built in fused_decode.hip; this file only sees these entry points
 bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits, float* out, int* ids_out,
                    float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err);
+bool moe_fused_multi_try(const moe_layer_desc* d, const float* x, const float* logits, int T, float* out,
+                         int* ids_out, float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err);
 
 static std::atomic<int> g_fused{1};
+
+#define FUSED_MAX_T 7  // the fused kernels take 1..7 tokens
 
 namespace {
 
@@ -47,7 +51,7 @@ Plan plan(const moe_layer_desc* d, int T) {
     const bool sh = d->s_gate != nullptr;
     p.NS = NU + (sh ? 1 : 0);
     p.tile = 64;
-    p.fused = moe_fused_scratch_bytes(d);
+    p.fused = moe_fused_scratch_bytes(d, T < FUSED_MAX_T ? T : FUSED_MAX_T);
     p.max_tiles = gpu_moe_max_tiles(T, NU, NE, p.tile);
     p.qx_k = r256((long long)T * E);
     p.qa_k = r256((long long)T * p.NS * FE);
@@ -109,10 +113,12 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
     const int E = d->n_embd, NE = d->n_expert, NU = d->n_used, FE = d->n_ff, type = d->type;
     const bool sh = d->s_gate != nullptr;
     const int mode = g_fused.load(std::memory_order_relaxed);
-    if (T == 1 && mode) {
+    if (T <= FUSED_MAX_T && mode) {
         hipError_t e = hipSuccess;
         const int kernels = mode == 1 ? 7 : mode & 7;
-        if (moe_fused_try(d, x, logits_in, out, ids_out, wts_out, scratch, kernels, st, &e)) return e;
+        if (T == 1 ? moe_fused_try(d, x, logits_in, out, ids_out, wts_out, scratch, kernels, st, &e)
+                   : moe_fused_multi_try(d, x, logits_in, T, out, ids_out, wts_out, scratch, kernels, st, &e))
+            return e;
     }
     const size_t rb_in = row_size(type, E), rb_out = row_size(type, FE);
     char* s = (char*)scratch;

@@ -144,19 +144,21 @@ __device__ __forceinline__ void router_select_wave(const float* lg, int ne, int 
 }
 
 // Softmax over ne (<= ROUTER_MAX_E) logits, the nu (<= 64) largest in descending order (ties to the lower index),
-// weights renormalised by max(sum, 6.103515625e-5). Wave 0 of the 256-thread workgroup selects; it writes
-// id_row[0..nu) and wts[0..nu) (any memory), visible to the whole workgroup on return.
+// weights renormalised by max(sum, 6.103515625e-5). router_select: wave 0 of the workgroup selects; it writes
+// id_row[0..nu) and wts[0..nu) (any memory), visible to the whole workgroup on return. router_select_one_wave:
+// the calling wave selects (no workgroup barrier).
+__device__ __forceinline__ void router_select_one_wave(const float* lg, int ne, int nu, int* id_row, float* wts) {
+    if (ne <= 128)
+        router_select_wave<2>(lg, ne, nu, id_row, wts);
+    else if (ne <= 256)
+        router_select_wave<4>(lg, ne, nu, id_row, wts);
+    else if (ne <= 512)
+        router_select_wave<8>(lg, ne, nu, id_row, wts);
+    else
+        router_select_wave<16>(lg, ne, nu, id_row, wts);
+}
 __device__ __forceinline__ void router_select(const float* lg, int ne, int nu, int* id_row, float* wts) {
-    if (threadIdx.x < 64) {
-        if (ne <= 128)
-            router_select_wave<2>(lg, ne, nu, id_row, wts);
-        else if (ne <= 256)
-            router_select_wave<4>(lg, ne, nu, id_row, wts);
-        else if (ne <= 512)
-            router_select_wave<8>(lg, ne, nu, id_row, wts);
-        else
-            router_select_wave<16>(lg, ne, nu, id_row, wts);
-    }
+    if (threadIdx.x < 64) router_select_one_wave(lg, ne, nu, id_row, wts);
     __syncthreads();
 }
 
