@@ -10,6 +10,8 @@
  */
 #include "moe_oracle.h"
 
+#include <omp.h>
+
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -362,6 +364,7 @@ void orc_matvec(int type, const void *W, size_t row_bytes, const float *x, float
 }
 
 void orc_matvec_f32(const float *W, const float *x, float *y, int n, int k) {
+#pragma omp parallel for schedule(static)
     for (int r = 0; r < n; ++r) {
         double acc = 0.0;
         for (int i = 0; i < k; ++i) acc += (double)W[(size_t)r * k + i] * (double)x[i];
@@ -504,12 +507,14 @@ static void expert_ffn(int type, const uint8_t *wg, const uint8_t *wu, const uin
     const size_t rb_in = orc_row_size(type, E), rb_out = orc_row_size(type, FE);
     float *g = (float *)malloc((size_t)FE * 4), *u = (float *)malloc((size_t)FE * 4);
     float *a = (float *)malloc((size_t)FE * 4), *ar = (float *)malloc((size_t)FE * 4);
+#pragma omp parallel for schedule(static)
     for (int r = 0; r < FE; ++r) {
         g[r] = (float)orc_row_dot_deq(type, wg + (size_t)r * rb_in, x_rt, E);
         u[r] = (float)orc_row_dot_deq(type, wu + (size_t)r * rb_in, x_rt, E);
     }
     orc_swiglu(g, u, a, FE);
     orc_q8_roundtrip(type, a, ar, FE);
+#pragma omp parallel for schedule(static)
     for (int i = 0; i < E; ++i) out[i] = (float)orc_row_dot_deq(type, wd + (size_t)i * rb_out, ar, FE);
     free(g);
     free(u);
@@ -557,4 +562,11 @@ int orc_moe_forward(const orc_moe_layer *L, const float *x, const float *logits_
     free(down);
     free(shared);
     return 0;
+}
+
+/* Threads of the row loops (OpenMP over output rows; every row is computed alone, so the results do not depend on
+ * the count). Returns the count in effect. */
+int orc_set_threads(int n) {
+    if (n > 0) omp_set_num_threads(n);
+    return omp_get_max_threads();
 }

@@ -102,6 +102,9 @@ typedef struct orc_moe_layer {
 int orc_moe_forward(const orc_moe_layer *L, const float *x, const float *logits_in, int t, float *out,
                     int32_t *ids_out, float *wts_out);
 
+/* OpenMP threads of the row loops (the results do not depend on the count); returns the count in effect */
+int orc_set_threads(int n);
+
 #ifdef __cplusplus
 }
 #endif

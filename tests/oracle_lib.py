@@ -41,6 +41,7 @@ class Oracle:
             "orc_max_tiles": (_I, [_I, _I, _I, _I]), "orc_swiglu": (None, [_P, _P, _P, _L]),
             "orc_combine": (None, [_P, _P, _P, _P, _P, _I, _I, _I]), "orc_rmsnorm": (None, [_P, _P, _P, _I, _F]),
             "orc_moe_forward": (_I, [ctypes.POINTER(Layer), _P, _P, _I, _P, _P, _P]),
+            "orc_set_threads": (_I, [_I]),
         }
         for k, (r, a) in sig.items():
             f = getattr(L, k)
