@@ -6,6 +6,7 @@
 
 #include "expert_units.h"
 #include "moe_layer.h"
+#include "q8_quant.h"
 #include "router_dev.h"
 
 #define FD_MAX_E 4096  // largest E the fused kernels take
@@ -31,6 +32,15 @@ struct FArgs {
     float* wts;
     int8_t* act_q;           // scratch [T][NS][FE]
     float* act_d;            // scratch [T][NS][FE / 32]
+    // Q4_K (T = 1): x's Q8_K bundle (written by kernel 1 through xo), the gate / up outputs in fp32, and down's
+    // input bundle (written by the SwiGLU kernel between kernels 2 and 3)
+    Q8Out xo;
+    float* g;                // scratch [NS][FE]
+    float* u;
+    float* act;
+    int8_t* aqk;             // down's input: Q8_K values [NS][FE], scales [NS][FE / 256], sums [NS][FE / 16]
+    float* adk;
+    int32_t* absk;
     unsigned long long* stamps;  // optional timestamps (profiling, one token): [workgroup][8], nullptr: none
     int T, E, NE, NU, FE, NS, has_gate;
 };
@@ -46,7 +56,7 @@ __device__ __forceinline__ void stamp(const FArgs& a, int k) {
 // shapes (gate / up K = E: lanes li, units ni; down K = FE: lo, no)
 bool moe_fused_prepare(const moe_layer_desc* d, FArgs& a);
 size_t moe_fused_scratch_bytes(const moe_layer_desc* d, int T);
-void moe_fused_carve(FArgs& a, void* scratch);
+char* moe_fused_carve(FArgs& a, void* scratch);
 void moe_mv_shape(int type, int K, int* lanes, int* units_per_lane);
 unsigned long long* moe_fused_stamps_ptr();  // the table moe_layer_fused_stamps set, or nullptr
 
@@ -55,8 +65,8 @@ unsigned long long* moe_fused_stamps_ptr();  // the table moe_layer_fused_stamps
 // r < nvalid are loaded; the others' results are undefined.
 template <int TYPE, int L, int R, int NUPL>
 __device__ __forceinline__ void rows_dot_multi(const uint8_t* const vr[R], const uint8_t* const sr[R],
-                                               const int8_t* const xq[R], const float* const xd[R], int nu, int gl,
-                                               int nvalid, float acc[R]) {
+                                               const int8_t* const xq[R], const float* const xd[R],
+                                               const int* const xbs[R], int nu, int gl, int nvalid, float acc[R]) {
     WUnit<TYPE> w[R][NUPL];
     XUnit<TYPE> x[R][NUPL];
 #pragma unroll
@@ -68,7 +78,7 @@ __device__ __forceinline__ void rows_dot_multi(const uint8_t* const vr[R], const
     for (int r = 0; r < R; ++r)
         if (r < nvalid)
 #pragma unroll
-            for (int i = 0; i < NUPL; ++i) load_x<TYPE>(xq[r], xd[r], nullptr, gl + i * L, x[r][i]);
+            for (int i = 0; i < NUPL; ++i) load_x<TYPE>(xq[r], xd[r], xbs[r], gl + i * L, x[r][i]);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         acc[r] = 0.0f;

@@ -16,6 +16,7 @@
 // 256-way atomic arrival cost ~10 us on MI355X, more than a kernel boundary.)
 
 #include "fused_common.h"
+#include "gpu_ops.h"
 #include "host_common.h"
 #include "moe_layer.h"
 #include "qmatvec.h"
@@ -26,7 +27,8 @@
 
 
 
-// ---- kernel 1: router logits (workgroups 0 .. NE - 1), x quantized (workgroup NE), the shared gate (NE + 1)
+// ---- kernel 1: router logits (workgroups 0 .. NE - 1), x quantized (workgroup NE; Q4_K: E / 256 workgroups),
+// the shared gate (the last workgroup)
 __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
     __shared__ float part[4];
     const int tid = threadIdx.x, E = a.E;
@@ -37,7 +39,16 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
         stamp(a, 1);
         return;
     }
-    if ((int)blockIdx.x == a.NE + 1) {  // the shared expert's gate
+    if (a.xo.qK) {  // Q4_K: one workgroup per 256-value block, the activation quantizer itself (Q8_0 and Q8_K)
+        __shared__ Q8Smem sh;
+        const int blk = blockIdx.x - a.NE;
+        if (blk < E / 256) {
+            q8_quantize_256(a.x[blk * 256 + tid], true, blk, tid, sh, a.xo);
+            stamp(a, 1);
+            return;
+        }
+    }
+    if ((int)blockIdx.x == a.NE + (a.xo.qK ? E / 256 : 1)) {  // the shared expert's gate
         const float g = shexp_gate(a.x, a.w_shexp, E, part);
         if (tid == 0) a.sg[0] = g;
         stamp(a, 1);
@@ -47,14 +58,19 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
     stamp(a, 1);
 }
 
-// ---- kernel 2: routing, then gate / up / SwiGLU / quantize of unit (slot, 32-row block)
-template <int TYPE, int NUPL_IN>
+// ---- kernel 2: routing, then gate / up / SwiGLU / quantize of unit (slot, 32-row block). 16 waves of 4 rows
+// (8 waves per matrix); a row is one group of L_IN lanes with NUPL_IN units per lane (the per-op shape for K = E),
+// so a wave holds 64 / L_IN groups of 4 L_IN / 64 rows. Q4_K writes gate / up in fp32 instead (its down input is
+// Q8_K, one scale per 256 values: the SwiGLU kernel between kernels 2 and 3 quantizes it).
+template <int TYPE, int L_IN, int NUPL_IN>
 __global__ void __launch_bounds__(64 * (64 / FD_GU_RW)) k_fd_gate_up(FArgs a) {
     constexpr int RW = FD_GU_RW, WPM = 32 / RW;  // rows per wave, waves per matrix
+    constexpr int G = 64 / L_IN, R = RW / G;     // lane groups per wave, rows per group
+    static_assert(R >= 1, "a wave's rows must cover its lane groups");
     __shared__ int s_ids[65];
     __shared__ float s_wts[64];
     __shared__ float gu[2][32];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, gl = lane & (L_IN - 1), grp = lane / L_IN;
     const int FE = a.FE, NU = a.NU, nbf = FE / 32;
     const int slot = blockIdx.x / nbf, b = blockIdx.x - slot * nbf;
     stamp(a, 2);
@@ -72,16 +88,26 @@ __global__ void __launch_bounds__(64 * (64 / FD_GU_RW)) k_fd_gate_up(FArgs a) {
     const long long rbase = e >= 0 ? (long long)e * FE : 0;
     const uint8_t* vb = a.v[mi] + rbase * a.vrb_in;
     const uint8_t* sb = a.s[mi] + rbase * a.srb_in;
-    float acc[RW];
-    rows_dot<TYPE, true, 64, RW, NUPL_IN>(vb, sb, a.vrb_in, a.srb_in, 32 * b + RW * (w % WPM), 1, FE, a.xq, a.xd,
-                                          nullptr, a.E, lane, acc);
-    if (lane == 0)
+    const int r0 = RW * (w % WPM) + grp * R;  // this group's first row of the unit's 32
+    constexpr bool Q8K = Fmt<TYPE>::Q8K;
+    float acc[R];
+    rows_dot<TYPE, true, L_IN, R, NUPL_IN>(vb, sb, a.vrb_in, a.srb_in, 32 * b + r0, 1, FE, Q8K ? a.xo.qK : a.xq,
+                                           Q8K ? a.xo.dK : a.xd, Q8K ? a.xo.bsK : nullptr, a.E, gl, acc);
+    if constexpr (Q8K) {
+        if (gl == 0)
 #pragma unroll
-        for (int r = 0; r < RW; ++r) gu[mat][RW * (w % WPM) + r] = acc[r];
-    __syncthreads();
-    stamp(a, 7);
-    if (w == 0)  // SwiGLU and the Q8_0 block of these 32 values
-        swiglu_q8_block(gu[0], gu[1], a.act_q + (long long)slot * FE + 32 * b, a.act_d + (long long)slot * nbf + b);
+            for (int r = 0; r < R; ++r) (mat ? a.u : a.g)[(long long)slot * FE + 32 * b + r0 + r] = acc[r];
+        stamp(a, 7);
+    } else {
+        if (gl == 0)
+#pragma unroll
+            for (int r = 0; r < R; ++r) gu[mat][r0 + r] = acc[r];
+        __syncthreads();
+        stamp(a, 7);
+        if (w == 0)  // SwiGLU and the Q8_0 block of these 32 values
+            swiglu_q8_block(gu[0], gu[1], a.act_q + (long long)slot * FE + 32 * b,
+                            a.act_d + (long long)slot * nbf + b);
+    }
     stamp(a, 4);
 }
 
@@ -101,10 +127,12 @@ __global__ void __launch_bounds__(1024) k_fd_down(FArgs a) {
     const int mi = e >= 0 ? 2 : 5;
     const uint8_t* vr[1] = {a.v[mi] + row * a.vrb_out};
     const uint8_t* sr[1] = {a.s[mi] + row * a.srb_out};
-    const int8_t* xq[1] = {a.act_q + (long long)slot * FE};
-    const float* xd[1] = {a.act_d + (long long)slot * (FE / 32)};
+    constexpr bool Q8K = Fmt<TYPE>::Q8K;
+    const int8_t* xq[1] = {Q8K ? a.aqk + (long long)slot * FE : a.act_q + (long long)slot * FE};
+    const float* xd[1] = {Q8K ? a.adk + (long long)slot * (FE / 256) : a.act_d + (long long)slot * (FE / 32)};
+    const int* xbs[1] = {Q8K ? a.absk + (long long)slot * (FE / 16) : nullptr};
     float acc[1];
-    rows_dot_multi<TYPE, L_OUT, 1, NUPL_OUT>(vr, sr, xq, xd, FE / 32, gl, 1, acc);
+    rows_dot_multi<TYPE, L_OUT, 1, NUPL_OUT>(vr, sr, xq, xd, xbs, fmt_units(TYPE, FE), gl, 1, acc);
     if (gl == 0) downv[slot][i] = acc[0];
     __syncthreads();
     if (tid < RB) {  // the combine kernel's expression
@@ -123,32 +151,43 @@ bool moe_packed_planes(const void* W, int type, int K, size_t row_bytes, const u
 
 namespace {
 
-// kernels: bit 0, 1, 2 launch kernel 1, 2, 3 (7 in normal use; a subset only for profiling one kernel)
-template <int TYPE, int NI, int LO, int NO>
-hipError_t launch_fused(const FArgs& a, int kernels, hipStream_t st) {
+// kernels: bit 0, 1, 2 launch kernel 1, 2 (with Q4_K's SwiGLU), 3 (7 in normal use; a subset only for profiling)
+template <int TYPE, int LI, int NI, int LO, int NO>
+hipError_t launch_fused(const FArgs& a, const qmatvec_q8* qa, int kernels, hipStream_t st) {
     hipError_t e = hipSuccess;
-    if (kernels & 1) e = launch_kernel(k_fd_logits, dim3(a.NE + 1 + a.has_gate), dim3(256), 0, st, a);
+    const int nq = Fmt<TYPE>::Q8K ? a.E / 256 : 1;  // quantizing workgroups of kernel 1
+    if (kernels & 1) e = launch_kernel(k_fd_logits, dim3(a.NE + nq + a.has_gate), dim3(256), 0, st, a);
     if (e == hipSuccess && (kernels & 2))
-        e = launch_kernel(k_fd_gate_up<TYPE, NI>, dim3(a.NS * (a.FE / 32)), dim3(64 * (64 / FD_GU_RW)), 0, st, a);
+        e = launch_kernel(k_fd_gate_up<TYPE, LI, NI>, dim3(a.NS * (a.FE / 32)), dim3(64 * (64 / FD_GU_RW)), 0, st,
+                          a);
+    if (Fmt<TYPE>::Q8K && e == hipSuccess && (kernels & 2))
+        e = gpu_swiglu(a.g, a.u, a.act, a.NS * a.FE, qa, st);
     if (e == hipSuccess && (kernels & 4))
         e = launch_kernel(k_fd_down<TYPE, LO, NO>, dim3(a.E / (64 / LO)), dim3(64 * a.NS), 0, st, a);
     return e;
 }
 
-// Gate / up: 64 lanes per row, NI units per lane (K = E = 2048 or 4096). Down: the per-operation kernel's
-// (lanes, units) for K = FE: 512 -> (16, 1), 768 -> (8, 3), 1024 -> (32, 1), 1536 -> (16, 3), 2048 -> (64, 1).
+// Gate / up: the per-operation (lanes, units) for K = E: 2048 -> (64, 1), 4096 -> (64, 2); Q4_K 3072 -> (16, 3).
+// Down, for K = FE: 512 -> (16, 1), 768 -> (8, 3), 1024 -> (32, 1), 1536 -> (16, 3), 2048 -> (64, 1); Q4_K 1024
+// -> (16, 1).
 template <int TYPE>
-hipError_t launch_fused_t(const FArgs& a, int ni, int lo, int no, int kernels, hipStream_t st) {
+hipError_t launch_fused_t(const FArgs& a, const qmatvec_q8* qa, int li, int ni, int lo, int no, int kernels,
+                          hipStream_t st) {
 #define FD_CASE(I, L, O) \
-    if (ni == I && lo == L && no == O) return launch_fused<TYPE, I, L, O>(a, kernels, st);
-    FD_CASE(1, 16, 1) FD_CASE(1, 8, 3) FD_CASE(1, 32, 1) FD_CASE(1, 16, 3) FD_CASE(1, 64, 1)
-    FD_CASE(2, 16, 1) FD_CASE(2, 8, 3) FD_CASE(2, 32, 1) FD_CASE(2, 16, 3) FD_CASE(2, 64, 1)
+    if (li == 64 && ni == I && lo == L && no == O) return launch_fused<TYPE, 64, I, L, O>(a, qa, kernels, st);
+    if constexpr (TYPE == QT_Q4_K) {
+        if (li == 16 && ni == 3 && lo == 16 && no == 1) return launch_fused<TYPE, 16, 3, 16, 1>(a, qa, kernels, st);
+    } else {
+        FD_CASE(1, 16, 1) FD_CASE(1, 8, 3) FD_CASE(1, 32, 1) FD_CASE(1, 16, 3) FD_CASE(1, 64, 1)
+        FD_CASE(2, 16, 1) FD_CASE(2, 8, 3) FD_CASE(2, 32, 1) FD_CASE(2, 16, 3) FD_CASE(2, 64, 1)
+    }
 #undef FD_CASE
     return hipErrorInvalidDeviceFunction;
 }
 
-bool fused_shape_ok(int ni, int lo, int no) {
-    if (ni != 1 && ni != 2) return false;
+bool fused_shape_ok(int type, int li, int ni, int lo, int no) {
+    if (type == QT_Q4_K) return li == 16 && ni == 3 && lo == 16 && no == 1;
+    if (li != 64 || (ni != 1 && ni != 2)) return false;
     return (lo == 16 && no == 1) || (lo == 8 && no == 3) || (lo == 32 && no == 1) || (lo == 16 && no == 3) ||
            (lo == 64 && no == 1);
 }
@@ -159,15 +198,20 @@ namespace {
 size_t fa256(size_t v) { return (v + 255) & ~(size_t)255; }
 }
 
-// Scratch bytes of the three kernels for T tokens: logits, gates, quantized x, routing, the quantized down input
+// Scratch bytes of the three kernels for T tokens: logits, gates, quantized x, routing, the quantized down input;
+// Q4_K (T = 1) also x's activation bundle, gate / up / SwiGLU in fp32 and down's input bundle
 size_t moe_fused_scratch_bytes(const moe_layer_desc* d, int T) {
     const size_t NS = d->n_used + (d->s_gate ? 1 : 0), E = d->n_embd, t = T;
-    return fa256(t * d->n_expert * 4) + fa256(t * 4) + fa256(t * E) + fa256(t * E / 32 * 4) + 2 * fa256(t * 64 * 4) +
-           fa256(t * NS * d->n_ff) + fa256(t * NS * d->n_ff / 32 * 4);
+    size_t n = fa256(t * d->n_expert * 4) + fa256(t * 4) + fa256(t * E) + fa256(t * E / 32 * 4) +
+               2 * fa256(t * 64 * 4) + fa256(t * NS * d->n_ff) + fa256(t * NS * d->n_ff / 32 * 4);
+    if (d->type == QT_Q4_K)
+        n += fa256(qmatvec_q8_bytes((int)((E + 255) / 256 * 256))) + fa256(qmatvec_q8_bytes((int)(NS * d->n_ff))) +
+             3 * fa256(NS * d->n_ff * 4);
+    return n;
 }
 
-// The scratch pieces of a.T tokens (the layout moe_fused_scratch_bytes sizes)
-void moe_fused_carve(FArgs& a, void* scratch) {
+// The scratch pieces of a.T tokens (the layout moe_fused_scratch_bytes sizes); returns the end of the common part
+char* moe_fused_carve(FArgs& a, void* scratch) {
     char* p = (char*)scratch;
     const size_t t = a.T;
     a.logits = (float*)p;
@@ -185,22 +229,26 @@ void moe_fused_carve(FArgs& a, void* scratch) {
     a.act_q = (int8_t*)p;
     p += fa256(t * a.NS * a.FE);
     a.act_d = (float*)p;
+    p += fa256(t * a.NS * a.FE / 32 * 4);
+    return p;
 }
 
-// Whether the fused kernel takes this layer at T = 1: a Q8_0-activation type, every expert matrix registered in
-// split-plane form, and shapes the instantiations cover. Fills the kernel arguments.
+// Whether the fused kernels take this layer: a supported type, every expert matrix registered in split-plane
+// form, and shapes the instantiations cover. Fills the kernel arguments.
 bool moe_fused_prepare(const moe_layer_desc* d, FArgs& a) {
     const int type = d->type, E = d->n_embd, FE = d->n_ff, NU = d->n_used;
-    if (type != QT_Q8_0 && type != QT_ROCMFP4 && type != QT_ROCMFP4_FAST) return false;
-    if (E % 2048 || E > FD_MAX_E || FE % 256 || NU > 64 || d->n_expert > ROUTER_MAX_E) return false;
+    if (type != QT_Q8_0 && type != QT_ROCMFP4 && type != QT_ROCMFP4_FAST && type != QT_Q4_K) return false;
+    if (E % 256 || E > FD_MAX_E || FE % 256 || NU > 64 || d->n_expert > ROUTER_MAX_E) return false;
     int li, ni, lo, no;
     moe_mv_shape(type, E, &li, &ni);
     moe_mv_shape(type, FE, &lo, &no);
-    if (li != 64 || !fused_shape_ok(ni, lo, no)) return false;
+    if (!fused_shape_ok(type, li, ni, lo, no)) return false;
     const int NS = NU + (d->s_gate ? 1 : 0);
     if (NS > 16) return false;
-    const size_t rb_in = (size_t)E / 32 * (type == QT_Q8_0 ? 34 : type == QT_ROCMFP4 ? 18 : 17);
-    const size_t rb_out = (size_t)FE / 32 * (type == QT_Q8_0 ? 34 : type == QT_ROCMFP4 ? 18 : 17);
+    auto native_row = [type](size_t k) {
+        return type == QT_Q4_K ? k / 256 * 144 : k / 32 * (type == QT_Q8_0 ? 34 : type == QT_ROCMFP4 ? 18 : 17);
+    };
+    const size_t rb_in = native_row(E), rb_out = native_row(FE);
     const void* W[6] = {d->w_gate, d->w_up, d->w_down, d->s_gate, d->s_up, d->s_down};
     for (int i = 0; i < 6; ++i) {
         a.v[i] = a.s[i] = nullptr;
@@ -211,10 +259,10 @@ bool moe_fused_prepare(const moe_layer_desc* d, FArgs& a) {
         if (!moe_packed_planes(W[i], type, i % 3 == 2 ? FE : E, i % 3 == 2 ? rb_out : rb_in, &a.v[i], &a.s[i]))
             return false;
     }
-    a.vrb_in = type == QT_Q8_0 ? E : E / 2;
-    a.srb_in = type == QT_ROCMFP4_FAST ? E / 32 : E / 16;
-    a.vrb_out = type == QT_Q8_0 ? FE : FE / 2;
-    a.srb_out = type == QT_ROCMFP4_FAST ? FE / 32 : FE / 16;
+    a.vrb_in = fmt_value_row(type, E);
+    a.srb_in = fmt_scale_row(type, E);
+    a.vrb_out = fmt_value_row(type, FE);
+    a.srb_out = fmt_scale_row(type, FE);
     a.E = E;
     a.NE = d->n_expert;
     a.NU = NU;
@@ -228,14 +276,33 @@ bool moe_fused_prepare(const moe_layer_desc* d, FArgs& a) {
 
 hipError_t moe_fused_launch(const moe_layer_desc* d, FArgs& a, void* scratch, int kernels, hipStream_t st) {
     a.T = 1;
-    moe_fused_carve(a, scratch);
+    char* p = moe_fused_carve(a, scratch);
+    qmatvec_q8 qa = {};
+    if (d->type == QT_Q4_K) {  // x's bundle (kernel 1), fp32 gate / up / SwiGLU, down's input bundle
+        qmatvec_q8 qx = {};
+        const int kx = (a.E + 255) / 256 * 256, ka = a.NS * a.FE;
+        qmatvec_q8_bind(&qx, p, kx);
+        p += fa256(qmatvec_q8_bytes(kx));
+        qmatvec_q8_bind(&qa, p, ka);
+        p += fa256(qmatvec_q8_bytes(ka));
+        a.xo = {qx.q0, qx.d0, qx.qK, qx.dK, qx.bsK, qx.s0, nullptr, 0};
+        a.g = (float*)p;
+        p += fa256((size_t)ka * 4);
+        a.u = (float*)p;
+        p += fa256((size_t)ka * 4);
+        a.act = (float*)p;
+        a.aqk = qa.qK;
+        a.adk = qa.dK;
+        a.absk = qa.bsK;
+    }
     int li, ni, lo, no;
     moe_mv_shape(d->type, a.E, &li, &ni);
     moe_mv_shape(d->type, a.FE, &lo, &no);
     switch (d->type) {
-    case QT_Q8_0: return launch_fused_t<QT_Q8_0>(a, ni, lo, no, kernels, st);
-    case QT_ROCMFP4: return launch_fused_t<QT_ROCMFP4>(a, ni, lo, no, kernels, st);
-    default: return launch_fused_t<QT_ROCMFP4_FAST>(a, ni, lo, no, kernels, st);
+    case QT_Q8_0: return launch_fused_t<QT_Q8_0>(a, &qa, li, ni, lo, no, kernels, st);
+    case QT_ROCMFP4: return launch_fused_t<QT_ROCMFP4>(a, &qa, li, ni, lo, no, kernels, st);
+    case QT_ROCMFP4_FAST: return launch_fused_t<QT_ROCMFP4_FAST>(a, &qa, li, ni, lo, no, kernels, st);
+    default: return launch_fused_t<QT_Q4_K>(a, &qa, li, ni, lo, no, kernels, st);
     }
 }
 

@@ -279,7 +279,7 @@ hipError_t launch_multi_t(const FArgs& a, int ni, int lo, int no, int kernels, h
 // T = 2..FD_MAX_T tokens through the multi-token kernels, when moe_fused_prepare takes the layer
 bool moe_fused_multi_try(const moe_layer_desc* d, const float* x, const float* logits, int T, float* out,
                          int* ids_out, float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err) {
-    if (T < 2 || T > FD_MAX_T) return false;
+    if (T < 2 || T > FD_MAX_T || d->type == QT_Q4_K) return false;  // (Q4_K: the per-operation path)
     FArgs a = {};
     if (!moe_fused_prepare(d, a)) return false;
     if (a.NS > 17 || T * a.NU > 64) return false;  // (the union and the per-token slot tables' sizes)
