@@ -535,9 +535,13 @@ hipError_t moe_launch_entries(int type, const void* W, size_t row_bytes, const q
     return hipErrorInvalidDeviceFunction;
 }
 
+int moe_grouped_mfma_tile(void);
+
+// The MFMA kernel's tile where it can take the matrix (once registered), else the per-entry kernel's (any tile;
+// 64 keeps its grids filled)
 extern "C" int qmatvec_id_batch_tile(int type, int N, int K) {
-    (void)N;
-    return qmatvec_q8_supported(type, K) ? ENTRY_TILE : 16;
+    if (!qmatvec_q8_supported(type, K)) return 16;
+    return moe_grouped_mfma_ok(type, N, K) ? moe_grouped_mfma_tile() : ENTRY_TILE;
 }
 
 extern "C" int qmatvec_q8_id_batch_supported(int type, int K) { return qmatvec_q8_supported(type, K); }

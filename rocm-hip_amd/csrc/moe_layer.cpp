@@ -50,7 +50,8 @@ Plan plan(const moe_layer_desc* d, int T) {
     const int E = d->n_embd, NE = d->n_expert, NU = d->n_used, FE = d->n_ff;
     const bool sh = d->s_gate != nullptr;
     p.NS = NU + (sh ? 1 : 0);
-    p.tile = 64;
+    const int t_in = qmatvec_id_batch_tile(d->type, FE, E), t_out = qmatvec_id_batch_tile(d->type, E, FE);
+    p.tile = t_in < t_out ? t_in : t_out;  // one grouping serves gate / up and down
     p.fused = moe_fused_scratch_bytes(d, T < FUSED_MAX_T ? T : FUSED_MAX_T);
     p.max_tiles = gpu_moe_max_tiles(T, NU, NE, p.tile);
     p.qx_k = r256((long long)T * E);

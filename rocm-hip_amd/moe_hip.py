@@ -8,7 +8,7 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "librocm_hip_moe.so")
+LIB_PATH = os.environ.get("ROCM_HIP_MOE_LIB") or os.path.join(HERE, "librocm_hip_moe.so")  # (the variable: a build of the library elsewhere)
 
 QT_F32, QT_Q8_0, QT_Q4_K, QT_ROCMFP4, QT_ROCMFP4_FAST = 0, 8, 12, 100, 101
 TYPE_NAMES = {QT_Q8_0: "q8_0", QT_Q4_K: "q4_K", QT_ROCMFP4: "q4_0_rocmfp4", QT_ROCMFP4_FAST: "q4_0_rocmfp4_fast"}
