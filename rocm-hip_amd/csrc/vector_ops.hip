@@ -103,10 +103,24 @@ __global__ void __launch_bounds__(256) k_add_rmsnorm(const float* x_in, const fl
     const int t = threadIdx.x, row = blockIdx.x;
     const float* xr = x_in + (size_t)row * n;
     const float* ar = add ? add + (size_t)row * n : nullptr;
+    // rows of up to 4096 values stay in registers between the two passes (one read of x and add)
+    constexpr int KEEP = 16;
+    float keep[KEEP];
+    const bool kept = n <= 256 * KEEP;
     float ss = 0.0f;
-    for (int i = t; i < n; i += 256) {
-        const float v = ar ? xr[i] + ar[i] : xr[i];
-        ss += v * v;
+    if (kept) {
+#pragma unroll
+        for (int k = 0; k < KEEP; ++k) {
+            const int i = t + 256 * k;
+            keep[k] = i < n ? (ar ? xr[i] + ar[i] : xr[i]) : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < KEEP; ++k) ss += keep[k] * keep[k];
+    } else {
+        for (int i = t; i < n; i += 256) {
+            const float v = ar ? xr[i] + ar[i] : xr[i];
+            ss += v * v;
+        }
     }
     ss = wave_sum(ss);
     if ((t & 63) == 0) part[t >> 6] = ss;
@@ -114,18 +128,27 @@ __global__ void __launch_bounds__(256) k_add_rmsnorm(const float* x_in, const fl
     const float tot = (part[0] + part[1]) + (part[2] + part[3]);
     const float inv = 1.0f / sqrtf(tot / (float)n + eps);
     const int nb = (n + 255) / 256;
-    for (int b = 0; b < nb; ++b) {
+    auto block = [&](int b, float xv) {  // block b of 256 values: outputs, then the quantizer (uniform call)
         const int i = b * 256 + t;
         const bool act = i < n;
         float v = 0.0f;
         if (act) {
-            const float xv = ar ? xr[i] + ar[i] : xr[i];
             if (ar) x_out[(size_t)row * n + i] = xv;
             v = xv * inv * (w ? w[i] : 1.0f);
             y[(size_t)row * n + i] = v;
             half_copy(o, (long long)row * n + i, v);
         }
         q8_quantize_256(v, act, (long long)row * nb + b, t, sh, o);
+    };
+    if (kept) {
+#pragma unroll
+        for (int b = 0; b < KEEP; ++b)
+            if (b < nb) block(b, keep[b]);
+    } else {
+        for (int b = 0; b < nb; ++b) {
+            const int i = b * 256 + t;
+            block(b, i < n ? (ar ? xr[i] + ar[i] : xr[i]) : 0.0f);
+        }
     }
 }
 
