@@ -45,6 +45,10 @@ struct GArgs {
     const int* out_rows;  // nullptr: entry i writes output row tile_start + i
     long long ldy;        // output row stride
     int T;                // n_tiles == nullptr (dense): T rows of one matrix in tiles of GG_TILE
+    const uint8_t* v2;    // the up matrix's planes (gate / up / SwiGLU kernel)
+    const uint8_t* s2;
+    int8_t* aq;           // SwiGLU kernel: down's Q8_0 input, rows of N values (out_rows), and scales
+    float* ad;
 };
 
 #define GG_ROWS 128  // weight rows per workgroup (32 per wave)
@@ -53,6 +57,9 @@ struct GArgs {
 #endif
 #ifndef GG_KB
 #define GG_KB 8  // blocks of 32 values per stage (4 or 8)
+#endif
+#ifndef GG_KB2
+#define GG_KB2 4  // the same for the gate / up / SwiGLU kernel (two matrices per stage)
 #endif
 #define GG_NT (GG_TILE / 32)
 
@@ -80,10 +87,11 @@ __device__ __forceinline__ void acc_block(v16f& acc, const v16i& I, const v16f& 
 // The weight rows' scale bytes come through registers.
 typedef __attribute__((address_space(3))) void lds_void;
 
-struct GBuf {  // one stage of operands
-    uint8_t a[4][GG_KB][1024];        // [wave][block][lane * 16]
-    uint8_t b[GG_KB][GG_NT][1024];    // [block][entry tile][lane * 16]
-    float dx[GG_KB / 4][GG_TILE][4];  // [block / 4][entry][block % 4]
+template <int NM, int KB>
+struct GBuf {  // one stage of operands of NM weight matrices sharing the activations
+    uint8_t a[NM][4][KB][1024];     // [matrix][wave][block][lane * 16]
+    uint8_t b[KB][GG_NT][1024];     // [block][entry tile][lane * 16]
+    float dx[KB / 4][GG_TILE][4];   // [block / 4][entry][block % 4]
 };
 
 __device__ __forceinline__ void lds_load16(const void* g, void* lds_run) {
@@ -99,95 +107,109 @@ __device__ __forceinline__ void wait_vm() {
 // Issue one stage's loads into B (see above); the weight scales of the stage go to wsc. Wave w loads the
 // activations of entry tile w % GG_NT, blocks w / GG_NT, + 4 / GG_NT, ... (xrow: its lane's entry row), and the
 // scales of entries GG_TILE / 4 w .. (dxr: its lane's entry row)
-template <int TYPE>
-__device__ __forceinline__ void g_issue(GBuf& B, int b0, uint4& wsc, const uint8_t* vrow, const uint8_t* srow,
-                                        const int8_t* xrow, const float* dxr, int nb, int w, int l, int kh) {
+template <int TYPE, int NM, int KB>
+__device__ __forceinline__ void g_issue(GBuf<NM, KB>& B, int b0, uint4 (&wsc)[NM], const uint8_t* const (&vrow)[NM],
+                                        const uint8_t* const (&srow)[NM], const int8_t* xrow, const float* dxr, int nb,
+                                        int w, int l, int kh) {
     constexpr int ES = GG_TILE / 4;  // entries whose scales one wave loads
 #pragma unroll
-    for (int bb = 0; bb < GG_KB; ++bb) {
-        const uint8_t* g = TYPE == QT_Q8_0 ? vrow + 16 * (kh ? nb + b0 + bb : b0 + bb) : vrow + 16 * (b0 + bb);
-        lds_load16(g, B.a[w][bb]);
-    }
+    for (int m = 0; m < NM; ++m)
 #pragma unroll
-    for (int j = 0; j < GG_KB * GG_NT / 4; ++j) {
+        for (int bb = 0; bb < KB; ++bb) {
+            const uint8_t* g =
+                TYPE == QT_Q8_0 ? vrow[m] + 16 * (kh ? nb + b0 + bb : b0 + bb) : vrow[m] + 16 * (b0 + bb);
+            lds_load16(g, B.a[m][w][bb]);
+        }
+#pragma unroll
+    for (int j = 0; j < KB * GG_NT / 4; ++j) {
         const int bb = w / GG_NT + (4 / GG_NT) * j;
         lds_load16(xrow + 32 * (b0 + bb), B.b[bb][w % GG_NT]);
     }
 #pragma unroll
-    for (int q = 0; q < GG_KB / 4; ++q)
+    for (int q = 0; q < KB / 4; ++q)
         if (l < ES) lds_load16(dxr + b0 + 4 * q, &B.dx[q][ES * w][0]);  // (lanes ES.. idle)
-    if constexpr (TYPE == QT_ROCMFP4_FAST) {  // 1 scale byte per block
-        if constexpr (GG_KB == 4)
-            wsc = make_uint4(*(const uint32_t*)(srow + b0), 0u, 0u, 0u);
-        else
-            wsc = make_uint4(((const uint2*)(srow + b0))->x, ((const uint2*)(srow + b0))->y, 0u, 0u);
-    } else {  // 2 scale bytes per block
-        if constexpr (GG_KB == 4) {
-            const uint2 v = *(const uint2*)(srow + 2 * b0);
-            wsc = make_uint4(v.x, v.y, 0u, 0u);
-        } else {
-            wsc = *(const uint4*)(srow + 2 * b0);
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+        if constexpr (TYPE == QT_ROCMFP4_FAST) {  // 1 scale byte per block
+            if constexpr (KB == 4)
+                wsc[m] = make_uint4(*(const uint32_t*)(srow[m] + b0), 0u, 0u, 0u);
+            else
+                wsc[m] = make_uint4(((const uint2*)(srow[m] + b0))->x, ((const uint2*)(srow[m] + b0))->y, 0u, 0u);
+        } else {  // 2 scale bytes per block
+            if constexpr (KB == 4) {
+                const uint2 v = *(const uint2*)(srow[m] + 2 * b0);
+                wsc[m] = make_uint4(v.x, v.y, 0u, 0u);
+            } else {
+                wsc[m] = *(const uint4*)(srow[m] + 2 * b0);
+            }
         }
     }
 }
 
 // The MFMAs of one stage from B
-template <int TYPE>
-__device__ __forceinline__ void g_compute(const GBuf& B, const uint4& wsc, v16f (&acc)[GG_NT], int w, int l, int lr,
-                                          int kh) {
+template <int TYPE, int NM, int KB>
+__device__ __forceinline__ void g_compute(const GBuf<NM, KB>& B, const uint4 (&wsc)[NM], v16f (&acc)[NM][GG_NT], int w,
+                                          int l, int lr, int kh) {
     const v16i zi = {};
 #pragma unroll
-    for (int bb = 0; bb < GG_KB; ++bb) {
+    for (int bb = 0; bb < KB; ++bb) {
         float dx[GG_NT];
 #pragma unroll
         for (int t = 0; t < GG_NT; ++t) dx[t] = B.dx[bb >> 2][32 * t + lr][bb & 3];
-        const uint32_t w2 = bb < 2 ? wsc.x : bb < 4 ? wsc.y : bb < 6 ? wsc.z : wsc.w;  // 2-byte scales
-        const uint32_t w1 = bb < 4 ? wsc.x : wsc.y;                                  // 1-byte scales
-        const uint8_t* arun = B.a[w][bb] + 16 * l;
-        if constexpr (TYPE == QT_ROCMFP4) {
-            const uint2 q = *(const uint2*)(arun + 8 * kh);  // bytes 8 kh .. 8 kh + 7 of the row's block
-            const uint32_t ew = w2 >> (16 * (bb & 1));
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint32_t sh = 4 * h;
-                const long A = (long)(((unsigned long)fp4x4_to_i8x4(q.y >> sh) << 32) | fp4x4_to_i8x4(q.x >> sh));
-                const float ee = ue4m3_half((ew >> (8 * h)) & 0xffu);
-                // B, K half kh of 16-value half h: bytes 16 h + 8 kh of the block = 8 bytes of the slot of the
-                // lane that loaded (entry, K half h)
+        for (int m = 0; m < NM; ++m) {
+            const uint32_t w2 = bb < 2 ? wsc[m].x : bb < 4 ? wsc[m].y : bb < 6 ? wsc[m].z : wsc[m].w;  // 2-byte
+            const uint32_t w1 = bb < 4 ? wsc[m].x : wsc[m].y;                                        // 1-byte
+            const uint8_t* arun = B.a[m][w][bb] + 16 * l;
+            if constexpr (TYPE == QT_ROCMFP4) {
+                const uint2 q = *(const uint2*)(arun + 8 * kh);  // bytes 8 kh .. 8 kh + 7 of the row's block
+                const uint32_t ew = w2 >> (16 * (bb & 1));
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t sh = 4 * h;
+                    const long A =
+                        (long)(((unsigned long)fp4x4_to_i8x4(q.y >> sh) << 32) | fp4x4_to_i8x4(q.x >> sh));
+                    const float ee = ue4m3_half((ew >> (8 * h)) & 0xffu);
+                    // B, K half kh of 16-value half h: bytes 16 h + 8 kh of the block = 8 bytes of the slot of the
+                    // lane that loaded (entry, K half h)
+#pragma unroll
+                    for (int t = 0; t < GG_NT; ++t) {
+                        const long Bt = *(const long*)(B.b[bb][t] + 16 * (lr + 32 * h) + 8 * kh);
+                        acc_block(acc[m][t], __builtin_amdgcn_mfma_i32_32x32x16_i8(A, Bt, zi, 0, 0, 0),
+                                  scale_outer(ee, dx[t], kh));
+                    }
+                }
+            } else {
+                const uint4 q = *(const uint4*)arun;
+                v4i A;
+                float dw;
+                if constexpr (TYPE == QT_Q8_0) {
+                    A = (v4i){(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+                    dw = h2f((uint16_t)(w2 >> (16 * (bb & 1))));
+                } else {  // FAST: K half kh = the low (0) or high (1) nibbles of the block's 16 bytes
+                    const uint32_t sh = kh ? 4 : 0;
+                    A = (v4i){(int)fp4x4_to_i8x4(q.x >> sh), (int)fp4x4_to_i8x4(q.y >> sh),
+                              (int)fp4x4_to_i8x4(q.z >> sh), (int)fp4x4_to_i8x4(q.w >> sh)};
+                    dw = ue4m3_half((w1 >> (8 * (bb & 3))) & 0xffu);
+                }
 #pragma unroll
                 for (int t = 0; t < GG_NT; ++t) {
-                    const long Bt = *(const long*)(B.b[bb][t] + 16 * (lr + 32 * h) + 8 * kh);
-                    acc_block(acc[t], __builtin_amdgcn_mfma_i32_32x32x16_i8(A, Bt, zi, 0, 0, 0),
-                              scale_outer(ee, dx[t], kh));
+                    const v4i Bt = *(const v4i*)(B.b[bb][t] + 16 * l);
+                    acc_block(acc[m][t], __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bt, zi, 0, 0, 0),
+                              scale_outer(dw, dx[t], kh));
                 }
-            }
-        } else {
-            const uint4 q = *(const uint4*)arun;
-            v4i A;
-            float dw;
-            if constexpr (TYPE == QT_Q8_0) {
-                A = (v4i){(int)q.x, (int)q.y, (int)q.z, (int)q.w};
-                dw = h2f((uint16_t)(w2 >> (16 * (bb & 1))));
-            } else {  // FAST: K half kh = the low (0) or high (1) nibbles of the block's 16 bytes
-                const uint32_t sh = kh ? 4 : 0;
-                A = (v4i){(int)fp4x4_to_i8x4(q.x >> sh), (int)fp4x4_to_i8x4(q.y >> sh), (int)fp4x4_to_i8x4(q.z >> sh),
-                          (int)fp4x4_to_i8x4(q.w >> sh)};
-                dw = ue4m3_half((w1 >> (8 * (bb & 3))) & 0xffu);
-            }
-#pragma unroll
-            for (int t = 0; t < GG_NT; ++t) {
-                const v4i Bt = *(const v4i*)(B.b[bb][t] + 16 * l);
-                acc_block(acc[t], __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bt, zi, 0, 0, 0),
-                          scale_outer(dw, dx[t], kh));
             }
         }
         __builtin_amdgcn_sched_barrier(0);
     }
 }
 
-template <int TYPE>
-__global__ void __launch_bounds__(256) k_grouped_mfma(GArgs a) {
-    __shared__ __attribute__((aligned(1024))) GBuf buf;
+// NM = 1: y rows (fp32) of one matrix. NM = 2, SwiGLU: gate (a.v) and up (a.v2) rows of the same block, then
+// act = SiLU(g) u (the swiglu kernel's expression) and its Q8_0 blocks -- a wave's 32 rows of one entry are one
+// block: 16 values in each of lanes l and l + 32 -- into a.aq / a.ad (the quantizer's expressions).
+template <int TYPE, int NM, int KB>
+__global__ void __launch_bounds__(256) k_grouped(GArgs a) {
+    __shared__ __attribute__((aligned(1024))) GBuf<NM, KB> buf;
     const int k = blockIdx.y;
     int e, st, cnt;
     if (a.n_tiles) {
@@ -205,44 +227,80 @@ __global__ void __launch_bounds__(256) k_grouped_mfma(GArgs a) {
     auto in_row = [&](int i) { return a.in_rows ? a.in_rows[st + i] : st + i; };
     auto out_row = [&](int i) { return a.out_rows ? a.out_rows[st + i] : st + i; };
     const int K = a.K, nb = K / 32;
-    // this lane's weight row (the launcher requires N % 128 == 0 and K % (32 GG_KB) == 0)
+    // this lane's weight row (the launcher requires N % 128 == 0 and K % (32 KB) == 0)
     const int r0 = blockIdx.x * GG_ROWS + 32 * w;
     const long long grow = (long long)e * a.N + r0 + lr;
-    const uint8_t* vrow = a.v + grow * a.vrb;
-    const uint8_t* srow = a.s + grow * a.srb;
+    const uint8_t* vrow[NM];
+    const uint8_t* srow[NM];
+    vrow[0] = a.v + grow * a.vrb;
+    srow[0] = a.s + grow * a.srb;
+    if constexpr (NM == 2) {
+        vrow[1] = a.v2 + grow * a.vrb;
+        srow[1] = a.s2 + grow * a.srb;
+    }
     // the entry rows this lane loads: activations of entry 32 (w % GG_NT) + lr, scales of entry GG_TILE / 4 w + l
     const int8_t* xrow = a.xq + (long long)in_row(min(32 * (w % GG_NT) + lr, cnt - 1)) * K + 16 * kh;
     const float* dxr = a.xd + (long long)in_row(min(GG_TILE / 4 * w + (l & (GG_TILE / 4 - 1)), cnt - 1)) * nb;
 
-    v16f acc[GG_NT];
+    v16f acc[NM][GG_NT];
 #pragma unroll
-    for (int t = 0; t < GG_NT; ++t) acc[t] = (v16f){};
-    const int nst = nb / GG_KB;
-    uint4 wsc;
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int t = 0; t < GG_NT; ++t) acc[m][t] = (v16f){};
+    const int nst = nb / KB;
+    uint4 wsc[NM];
     for (int s = 0; s < nst; ++s) {
         // one stage: its loads, then (with several workgroups per CU hiding the latency of each other's loads)
         // its MFMAs
-        g_issue<TYPE>(buf, s * GG_KB, wsc, vrow, srow, xrow, dxr, nb, w, l, kh);
+        g_issue<TYPE, NM, KB>(buf, s * KB, wsc, vrow, srow, xrow, dxr, nb, w, l, kh);
         wait_vm<0>();
         __syncthreads();
-        g_compute<TYPE>(buf, wsc, acc, w, l, lr, kh);
+        g_compute<TYPE, NM, KB>(buf, wsc, acc, w, l, lr, kh);
         __syncthreads();
     }
-    // acc[t][j] is C[row 8 (j / 4) + 4 kh + j % 4][entry 32 t + lr] of the wave's 32 x GG_TILE block
+    // acc[m][t][j] is C[row 8 (j / 4) + 4 kh + j % 4][entry 32 t + lr] of the wave's 32 x GG_TILE block
+    if constexpr (NM == 1) {
 #pragma unroll
-    for (int t = 0; t < GG_NT; ++t)
-        if (32 * t + lr < cnt) {
-            float* y = a.y + (long long)out_row(32 * t + lr) * a.ldy + r0;
+        for (int t = 0; t < GG_NT; ++t)
+            if (32 * t + lr < cnt) {
+                float* y = a.y + (long long)out_row(32 * t + lr) * a.ldy + r0;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) y[8 * (j >> 2) + 4 * kh + (j & 3)] = acc[t][j];
+                for (int j = 0; j < 16; ++j) y[8 * (j >> 2) + 4 * kh + (j & 3)] = acc[0][t][j];
+            }
+    } else {
+#pragma unroll
+        for (int t = 0; t < GG_NT; ++t) {
+            float act[16];
+            float am = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float g = acc[0][t][j];
+                act[j] = g / (1.0f + __expf(-g)) * acc[1][t][j];
+                am = fmaxf(am, fabsf(act[j]));
+            }
+            am = fmaxf(am, __shfl_xor(am, 32, 64));  // the block's other 16 rows
+            const float id = am != 0.0f ? 127.0f / am : 0.0f;
+            if (32 * t + lr < cnt) {
+                const long long pr = out_row(32 * t + lr);
+                int8_t* q = a.aq + pr * a.N + r0;
+#pragma unroll
+                for (int m4 = 0; m4 < 4; ++m4) {  // rows 8 m4 + 4 kh .. + 3: four consecutive bytes
+                    uint32_t pk = 0;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) pk |= ((uint32_t)(int)rintf(act[4 * m4 + c] * id) & 0xffu) << (8 * c);
+                    *(uint32_t*)(q + 8 * m4 + 4 * kh) = pk;
+                }
+                if (kh == 0) a.ad[pr * (a.N / 32) + r0 / 32] = __half2float(__float2half(am / 127.0f));
+            }
         }
+    }
 }
 
-// Whether the MFMA kernel takes this matrix: a split-plane type with Q8_0 activations, whole 128-row blocks and
-// whole K stages
+// Whether the MFMA kernels take this matrix: a split-plane type with Q8_0 activations, whole 128-row blocks and
+// whole K stages (of either kernel)
 bool moe_grouped_mfma_ok(int type, int N, int K) {
     return (type == QT_Q8_0 || type == QT_ROCMFP4 || type == QT_ROCMFP4_FAST) && N % GG_ROWS == 0 &&
-           K % (GG_KB * 32) == 0;
+           K % (GG_KB * 32) == 0 && K % (GG_KB2 * 32) == 0;
 }
 
 // The entry tile the MFMA kernel takes
@@ -252,12 +310,31 @@ hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s,
                                    const qmatvec_q8* q, float* y, int N, int K, int max_tiles, const int32_t* n_tiles,
                                    const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
                                    const int32_t* in_rows, const int32_t* out_rows, hipStream_t stream) {
-    GArgs a = {v, s, vrb, srb, q->q0, q->d0, y, N, K, n_tiles, tile_e, tile_start, tile_n, in_rows, out_rows, N, 0};
+    GArgs a = {v,      s,       vrb,      srb, q->q0, q->d0, y,       N,       K,       n_tiles, tile_e,
+               tile_start, tile_n, in_rows, out_rows, N, 0, nullptr, nullptr, nullptr, nullptr};
     const dim3 g(N / GG_ROWS, max_tiles), b(256);
     switch (type) {
-    case QT_Q8_0: return launch_kernel(k_grouped_mfma<QT_Q8_0>, g, b, 0, stream, a);
-    case QT_ROCMFP4: return launch_kernel(k_grouped_mfma<QT_ROCMFP4>, g, b, 0, stream, a);
-    case QT_ROCMFP4_FAST: return launch_kernel(k_grouped_mfma<QT_ROCMFP4_FAST>, g, b, 0, stream, a);
+    case QT_Q8_0: return launch_kernel(k_grouped<QT_Q8_0, 1, GG_KB>, g, b, 0, stream, a);
+    case QT_ROCMFP4: return launch_kernel(k_grouped<QT_ROCMFP4, 1, GG_KB>, g, b, 0, stream, a);
+    case QT_ROCMFP4_FAST: return launch_kernel(k_grouped<QT_ROCMFP4_FAST, 1, GG_KB>, g, b, 0, stream, a);
+    }
+    return hipErrorInvalidDeviceFunction;
+}
+
+// Gate and up of the same tiles in one launch, then SwiGLU and down's Q8_0 input (aq rows of N, ad per 32)
+// instead of the gate / up outputs
+hipError_t moe_launch_grouped_swiglu(int type, const uint8_t* vg, const uint8_t* sg, const uint8_t* vu,
+                                     const uint8_t* su, long long vrb, long long srb, const qmatvec_q8* q, int8_t* aq,
+                                     float* ad, int N, int K, int max_tiles, const int32_t* n_tiles,
+                                     const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
+                                     const int32_t* in_rows, const int32_t* out_rows, hipStream_t stream) {
+    GArgs a = {vg,         sg,     vrb,     srb,      q->q0, q->d0, nullptr, N,  K,  n_tiles, tile_e,
+               tile_start, tile_n, in_rows, out_rows, N,     0,     vu,      su, aq, ad};
+    const dim3 g(N / GG_ROWS, max_tiles), b(256);
+    switch (type) {
+    case QT_Q8_0: return launch_kernel(k_grouped<QT_Q8_0, 2, GG_KB2>, g, b, 0, stream, a);
+    case QT_ROCMFP4: return launch_kernel(k_grouped<QT_ROCMFP4, 2, GG_KB2>, g, b, 0, stream, a);
+    case QT_ROCMFP4_FAST: return launch_kernel(k_grouped<QT_ROCMFP4_FAST, 2, GG_KB2>, g, b, 0, stream, a);
     }
     return hipErrorInvalidDeviceFunction;
 }
@@ -266,12 +343,13 @@ hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s,
 hipError_t moe_launch_dense_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
                                  const qmatvec_q8* q, float* y, long long ldy, int N, int K, int T,
                                  hipStream_t stream) {
-    GArgs a = {v, s, vrb, srb, q->q0, q->d0, y, N, K, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, ldy, T};
+    GArgs a = {v,       s,       vrb,     srb,     q->q0, q->d0, y,       N,       K,       nullptr, nullptr,
+               nullptr, nullptr, nullptr, nullptr, ldy,   T,     nullptr, nullptr, nullptr, nullptr};
     const dim3 g(N / GG_ROWS, (T + GG_TILE - 1) / GG_TILE), b(256);
     switch (type) {
-    case QT_Q8_0: return launch_kernel(k_grouped_mfma<QT_Q8_0>, g, b, 0, stream, a);
-    case QT_ROCMFP4: return launch_kernel(k_grouped_mfma<QT_ROCMFP4>, g, b, 0, stream, a);
-    case QT_ROCMFP4_FAST: return launch_kernel(k_grouped_mfma<QT_ROCMFP4_FAST>, g, b, 0, stream, a);
+    case QT_Q8_0: return launch_kernel(k_grouped<QT_Q8_0, 1, GG_KB>, g, b, 0, stream, a);
+    case QT_ROCMFP4: return launch_kernel(k_grouped<QT_ROCMFP4, 1, GG_KB>, g, b, 0, stream, a);
+    case QT_ROCMFP4_FAST: return launch_kernel(k_grouped<QT_ROCMFP4_FAST, 1, GG_KB>, g, b, 0, stream, a);
     }
     return hipErrorInvalidDeviceFunction;
 }

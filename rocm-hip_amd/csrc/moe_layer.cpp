@@ -19,6 +19,14 @@ bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits,
 bool moe_fused_multi_try(const moe_layer_desc* d, const float* x, const float* logits, int T, float* out,
                          int* ids_out, float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err);
 
+bool moe_packed_planes(const void* W, int type, int K, size_t row_bytes, const uint8_t** v, const uint8_t** s);
+bool moe_grouped_mfma_ok(int type, int N, int K);
+hipError_t moe_launch_grouped_swiglu(int type, const uint8_t* vg, const uint8_t* sg, const uint8_t* vu,
+                                     const uint8_t* su, long long vrb, long long srb, const qmatvec_q8* q, int8_t* aq,
+                                     float* ad, int N, int K, int max_tiles, const int32_t* n_tiles,
+                                     const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
+                                     const int32_t* in_rows, const int32_t* out_rows, hipStream_t stream);
+
 static std::atomic<int> g_fused{1};
 
 #define FUSED_MAX_T 7  // the fused kernels take 1..7 tokens
@@ -27,6 +35,10 @@ namespace {
 
 size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
 int r256(long long k) { return (int)((k + 255) / 256 * 256); }
+
+// Split-plane row bytes (values, scales) of the Q8_0-activation types (8: Q8_0, 100: ROCmFP4, 101: FAST)
+long long value_row(int type, int k) { return type == 8 ? k : k / 2; }
+long long scale_row(int type, int k) { return type == 101 ? k / 32 : k / 16; }
 
 size_t row_size(int type, int k) {
     switch (type) {
@@ -171,11 +183,21 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
         int* ts = (int*)(s + p.ts);
         int* tn = (int*)(s + p.tn);
         CHECK(gpu_moe_group(ids, T, NU, NE, p.tile, tok, pair, ntile, te, ts, tn, st));
-        CHECK(qmatvec_launch_q8_id_batch(type, d->w_gate, rb_in, &qx, g, FE, E, p.max_tiles, p.tile, ntile, te, ts,
-                                         tn, tok, pair, st));
-        CHECK(qmatvec_launch_q8_id_batch(type, d->w_up, rb_in, &qx, u, FE, E, p.max_tiles, p.tile, ntile, te, ts, tn,
-                                         tok, pair, st));
-        CHECK(gpu_swiglu(g, u, act, T * NU * FE, &qa, st));
+        const uint8_t *vg = nullptr, *sgp = nullptr, *vu = nullptr, *sup = nullptr, *vd = nullptr, *sdp = nullptr;
+        if (mode && moe_grouped_mfma_ok(type, FE, E) && moe_grouped_mfma_ok(type, E, FE) &&
+            moe_packed_planes(d->w_gate, type, E, rb_in, &vg, &sgp) &&
+            moe_packed_planes(d->w_up, type, E, rb_in, &vu, &sup) &&
+            moe_packed_planes(d->w_down, type, FE, rb_out, &vd, &sdp)) {
+            // gate, up, SwiGLU and down's Q8_0 input in one launch (the same bits as the three launches below)
+            CHECK(moe_launch_grouped_swiglu(type, vg, sgp, vu, sup, value_row(type, E), scale_row(type, E), &qx, qa.q0,
+                                            qa.d0, FE, E, p.max_tiles, ntile, te, ts, tn, tok, pair, st));
+        } else {
+            CHECK(qmatvec_launch_q8_id_batch(type, d->w_gate, rb_in, &qx, g, FE, E, p.max_tiles, p.tile, ntile, te,
+                                             ts, tn, tok, pair, st));
+            CHECK(qmatvec_launch_q8_id_batch(type, d->w_up, rb_in, &qx, u, FE, E, p.max_tiles, p.tile, ntile, te, ts,
+                                             tn, tok, pair, st));
+            CHECK(gpu_swiglu(g, u, act, T * NU * FE, &qa, st));
+        }
         CHECK(qmatvec_launch_q8_id_batch(type, d->w_down, rb_out, &qa, down, E, FE, p.max_tiles, p.tile, ntile, te,
                                          ts, tn, pair, pair, st));
         if (!sh) CHECK(gpu_moe_combine(down, wts, nullptr, nullptr, out, NU, E, T, st));
