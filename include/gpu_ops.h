@@ -55,6 +55,14 @@ static inline int gpu_moe_max_tiles(int T, int n_used, int n_expert, int tile) {
 hipError_t gpu_moe_group(const int* ids, int T, int n_used, int n_expert, int tile, int* tok_rows, int* pair_rows,
                          int* n_tiles, int* tile_e, int* tile_start, int* tile_n, hipStream_t stream);
 
+// No counterpart in the reference (additive). gpu_moe_group with a caller workspace of gpu_moe_group_ws_bytes(T,
+// n_expert) bytes (4-byte aligned): the same outputs bit for bit, from several workgroups (per-block counts, one
+// scan, per-block placement) instead of one.
+size_t gpu_moe_group_ws_bytes(int T, int n_expert);
+hipError_t gpu_moe_group_ws(const int* ids, int T, int n_used, int n_expert, int tile, int* tok_rows,
+                            int* pair_rows, int* n_tiles, int* tile_e, int* tile_start, int* tile_n, void* ws,
+                            size_t ws_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -140,6 +140,147 @@ __global__ void __launch_bounds__(64 * GROUP_WAVES) k_moe_group(const int* ids, 
     }
 }
 
+// ---- Several workgroups, with a workspace (gpu_moe_group_ws): the same outputs. Tokens in blocks of 256 (4
+// waves, one token per lane).
+//   k_group_count: per block, the 64-bit expert masks of its 4 waves, then per expert the block's entry count
+//                  into ws[block][expert];
+//   k_group_scan:  one workgroup: per expert the exclusive scan over the blocks (ws becomes each block's offset
+//                  within the expert's run) and the total, then the scans over the experts and the tile table
+//                  (k_moe_group's code) and the experts' first entries into eoff;
+//   k_group_place: per block, the masks again, the wave prefixes, and each entry's position: eoff + the block's
+//                  offset + the wave prefix + the popcount of its wave's mask below its lane.
+#define GB_WAVES 4
+
+__device__ __forceinline__ void block_masks(const int* ids, int T, int nu, int ne, unsigned long long* masks, int t,
+                                            uint64_t& vm) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    unsigned long long* my = masks + (size_t)w * ne;
+    for (int e = lane; e < ne; e += 64) my[e] = 0ull;
+    __syncthreads();
+    const int* row = ids + (size_t)t * nu;
+    vm = t < T ? group_valid_mask(row, nu, ne) : 0ull;
+    for (int j = 0; j < nu; ++j)
+        if ((vm >> j) & 1) atomicOr(&my[row[j]], 1ull << lane);
+    __syncthreads();
+}
+
+__global__ void __launch_bounds__(64 * GB_WAVES) k_group_count(const int* ids, int T, int nu, int ne, int* ws) {
+    extern __shared__ unsigned long long g_smem[];
+    uint64_t vm;
+    block_masks(ids, T, nu, ne, g_smem, blockIdx.x * 64 * GB_WAVES + threadIdx.x, vm);
+    for (int e = threadIdx.x; e < ne; e += 64 * GB_WAVES) {
+        int s = 0;
+#pragma unroll
+        for (int k = 0; k < GB_WAVES; ++k) s += __popcll(g_smem[(size_t)k * ne + e]);
+        ws[(size_t)blockIdx.x * ne + e] = s;
+    }
+}
+
+__global__ void __launch_bounds__(1024) k_group_scan(int* ws, int nblk, int ne, int tile, int* eoff_out, int* n_tiles,
+                                                     int* tile_e, int* tile_start, int* tile_n) {
+    __shared__ int cnt[1024];
+    __shared__ int wpart[2][16];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    if (tid < ne) {  // the blocks' offsets within the expert's run, the expert's total
+        int off = 0;
+        for (int b = 0; b < nblk; ++b) {
+            const int c = ws[(size_t)b * ne + tid];
+            ws[(size_t)b * ne + tid] = off;
+            off += c;
+        }
+        cnt[tid] = off;
+    }
+    __syncthreads();
+    const int c = tid < ne ? cnt[tid] : 0, nt = (c + tile - 1) / tile;
+    int a = c, bsum = nt;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int ua = __shfl_up(a, d, 64), ub = __shfl_up(bsum, d, 64);
+        if (lane >= d) {
+            a += ua;
+            bsum += ub;
+        }
+    }
+    if (lane == 63) {
+        wpart[0][w] = a;
+        wpart[1][w] = bsum;
+    }
+    __syncthreads();
+    int ba = 0, bb = 0;
+    for (int k = 0; k < w; ++k) {
+        ba += wpart[0][k];
+        bb += wpart[1][k];
+    }
+    const int eo = ba + a - c, to = bb + bsum - nt;
+    if (tid < ne) {
+        eoff_out[tid] = eo;
+        for (int k = 0; k < nt; ++k) {
+            tile_e[to + k] = tid;
+            tile_start[to + k] = eo + k * tile;
+            tile_n[to + k] = min(tile, c - k * tile);
+        }
+        if (tid == ne - 1) *n_tiles = to + nt;
+    }
+}
+
+__global__ void __launch_bounds__(64 * GB_WAVES) k_group_place(const int* ids, int T, int nu, int ne, const int* ws,
+                                                               const int* eoff, int* tok_rows, int* pair_rows) {
+    extern __shared__ unsigned long long g_smem[];
+    unsigned long long* masks = g_smem;
+    uint16_t* pre = (uint16_t*)(masks + (size_t)GB_WAVES * ne);  // [GB_WAVES][ne]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, t = blockIdx.x * 64 * GB_WAVES + tid;
+    uint64_t vm;
+    block_masks(ids, T, nu, ne, masks, t, vm);
+    for (int e = tid; e < ne; e += 64 * GB_WAVES) {
+        int s = 0;
+#pragma unroll
+        for (int k = 0; k < GB_WAVES; ++k) {
+            pre[(size_t)k * ne + e] = (uint16_t)s;
+            s += __popcll(masks[(size_t)k * ne + e]);
+        }
+    }
+    __syncthreads();
+    const int* row = ids + (size_t)t * nu;
+    const int* boff = ws + (size_t)blockIdx.x * ne;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    for (int j = 0; j < nu; ++j) {
+        if (!((vm >> j) & 1)) continue;
+        const int e = row[j];
+        const int p = eoff[e] + boff[e] + pre[(size_t)w * ne + e] + __popcll(masks[(size_t)w * ne + e] & below);
+        tok_rows[p] = t;
+        pair_rows[p] = t * nu + j;
+    }
+}
+
+extern "C" size_t gpu_moe_group_ws_bytes(int T, int n_expert) {
+    if (T <= 0 || n_expert <= 0) return 0;
+    const size_t nblk = ((size_t)T + 64 * GB_WAVES - 1) / (64 * GB_WAVES);
+    return (nblk + 1) * (size_t)n_expert * 4;
+}
+
+extern "C" hipError_t gpu_moe_group_ws(const int* ids, int T, int n_used, int n_expert, int tile, int* tok_rows,
+                                       int* pair_rows, int* n_tiles, int* tile_e, int* tile_start, int* tile_n,
+                                       void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (T <= 0 || n_used <= 0 || n_used > 64 || n_expert <= 0 || n_expert > 1024 || tile <= 0 ||
+        (long long)T * n_used > 0x7fffffffLL || !ws || ws_bytes < gpu_moe_group_ws_bytes(T, n_expert) ||
+        ((uintptr_t)ws & 3))
+        return hipErrorInvalidValue;
+    const int nblk = (T + 64 * GB_WAVES - 1) / (64 * GB_WAVES);
+    int* cnt = (int*)ws;
+    int* eoff = cnt + (size_t)nblk * n_expert;
+    const size_t shm_c = (size_t)GB_WAVES * n_expert * 8, shm_p = shm_c + (size_t)GB_WAVES * n_expert * 2;
+    hipError_t e = launch_kernel(k_group_count, dim3(nblk), dim3(64 * GB_WAVES), shm_c, stream, ids, T, n_used,
+                                 n_expert, cnt);
+    if (e == hipSuccess)
+        e = launch_kernel(k_group_scan, dim3(1), dim3(1024), 0, stream, cnt, nblk, n_expert, tile, eoff, n_tiles,
+                          tile_e, tile_start, tile_n);
+    if (e == hipSuccess)
+        e = launch_kernel(k_group_place, dim3(nblk), dim3(64 * GB_WAVES), shm_p, stream, ids, T, n_used, n_expert,
+                          (const int*)cnt, (const int*)eoff, tok_rows, pair_rows);
+    return e;
+}
+
 static size_t group_smem(int ne) {
     return (size_t)GROUP_WAVES * ne * 8 + (size_t)GROUP_WAVES * ne * 2 + 4 + 3 * (size_t)ne * 4;
 }

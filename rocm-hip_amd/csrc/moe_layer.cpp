@@ -53,7 +53,7 @@ size_t row_size(int type, int k) {
 // Scratch carve-up; every piece 256-byte aligned
 struct Plan {
     size_t fused, logits, ids, wts, sg, qx, g, u, act, qa, down, sg_, su, sact, qs, sout, tok, pair, ntile, te, ts, tn,
-        total;
+        gws, total;
     int NS, qx_k, qa_k, qs_k, max_tiles, tile;
 };
 
@@ -96,6 +96,7 @@ Plan plan(const moe_layer_desc* d, int T) {
     p.te = take((size_t)p.max_tiles * 4);
     p.ts = take((size_t)p.max_tiles * 4);
     p.tn = take((size_t)p.max_tiles * 4);
+    p.gws = take(gpu_moe_group_ws_bytes(T, NE));
     p.total = o;
     return p;
 }
@@ -182,7 +183,8 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
         int* te = (int*)(s + p.te);
         int* ts = (int*)(s + p.ts);
         int* tn = (int*)(s + p.tn);
-        CHECK(gpu_moe_group(ids, T, NU, NE, p.tile, tok, pair, ntile, te, ts, tn, st));
+        CHECK(gpu_moe_group_ws(ids, T, NU, NE, p.tile, tok, pair, ntile, te, ts, tn, s + p.gws,
+                               gpu_moe_group_ws_bytes(T, NE), st));
         const uint8_t *vg = nullptr, *sgp = nullptr, *vu = nullptr, *sup = nullptr, *vd = nullptr, *sdp = nullptr;
         if (mode && moe_grouped_mfma_ok(type, FE, E) && moe_grouped_mfma_ok(type, E, FE) &&
             moe_packed_planes(d->w_gate, type, E, rb_in, &vg, &sgp) &&

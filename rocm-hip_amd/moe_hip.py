@@ -70,6 +70,8 @@ SIGNATURES = {
     "gpu_moe_combine": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "gpu_moe_combine_scaled": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "gpu_moe_group": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
+    "gpu_moe_group_ws_bytes": (_Z, [_I, _I]),
+    "gpu_moe_group_ws": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _Z, _P]),
     "moe_layer_scratch_bytes": (_Z, [ctypes.c_void_p, _I]),
     "moe_layer_forward": (_I, [ctypes.c_void_p, _P, _P, _I, _P, _P, _P, _P, _Z, _P]),
     "moe_layer_set_fused": (None, [_I]),
