@@ -27,6 +27,8 @@ hipError_t moe_launch_grouped_swiglu(int type, const uint8_t* vg, const uint8_t*
                                      const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
                                      const int32_t* in_rows, const int32_t* out_rows, hipStream_t stream);
 
+hipError_t moe_quantize_q8_0(const float* x, int n, const qmatvec_q8* q, hipStream_t stream);
+
 static std::atomic<int> g_fused{1};
 
 #define FUSED_MAX_T 7  // the fused kernels take 1..7 tokens
@@ -153,7 +155,10 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
         lg = (float*)logits_in;
     else
         CHECK(qmatvec_launch_batch(0, d->w_router, (size_t)E * 4, x, lg, NE, E, T, st));
-    CHECK(qmatvec_quantize(x, T * E, &qx, st));
+    if (type == 12)  // Q4_K reads Q8_K activations; the others read Q8_0 values and scales only
+        CHECK(qmatvec_quantize(x, T * E, &qx, st));
+    else
+        CHECK(moe_quantize_q8_0(x, T * E, &qx, st));
 
     const bool slot = T == 1 && sh;  // moe_core_one: the shared expert as slot NU
     if (T < 8) {

@@ -8,6 +8,7 @@
 #include "gpu_ops.h"
 #include "host_common.h"
 #include "moe_common.h"
+#include "fused_common.h"
 #include "q8_quant.h"
 #include "qmatvec.h"
 #include "router_dev.h"
@@ -47,6 +48,13 @@ __global__ void __launch_bounds__(256) k_quantize_q8(const float* x, int n, Q8Ou
     const float v = act ? x[i] : 0.0f;
     if (act) half_copy(o, i, v);
     q8_quantize_256(v, act, blockIdx.x, t, sh, o);
+}
+
+// Q8_0 values and scales only (the Q8_0-activation types need no Q8_1 sums or Q8_K): 2,048 values per
+// workgroup, the quantizer's expressions (the same bits as k_quantize_q8's Q8_0 part)
+__global__ void __launch_bounds__(256) k_quantize_q8_0(const float* x, int n, int8_t* q0, float* d0) {
+    const int base = blockIdx.x * 2048;
+    quantize_row_q8_0(x + base, min(2048, n - base), q0 + base, d0 + base / 32);
 }
 
 // ------------------------------------------------------------------ SwiGLU (src/gpu_ops.hip:103-114)
@@ -311,4 +319,11 @@ extern "C" hipError_t gpu_moe_combine_scaled(const float* down, const float* wts
 extern "C" hipError_t gpu_moe_combine(const float* down, const float* wts, const float* shared, const float* sg,
                                       float* out, int n_used, int n, int T, hipStream_t stream) {
     return gpu_moe_combine_scaled(down, wts, shared, sg, nullptr, nullptr, out, n_used, n, T, stream);
+}
+
+// Internal (moe_layer_forward): Q8_0 values and scales of x [n] into q (n % 32 == 0, n <= q->max_k)
+hipError_t moe_quantize_q8_0(const float* x, int n, const qmatvec_q8* q, hipStream_t stream) {
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (n <= 0 || n % 32 || !q || n > q->max_k) return hipErrorInvalidValue;
+    return launch_kernel(k_quantize_q8_0, dim3((n + 2047) / 2048), dim3(256), 0, stream, x, n, q->q0, q->d0);
 }
