@@ -76,6 +76,52 @@ SIGNATURES = {
     "moe_layer_forward": (_I, [ctypes.c_void_p, _P, _P, _I, _P, _P, _P, _P, _Z, _P]),
     "moe_layer_set_fused": (None, [_I]),
     "moe_layer_fused_stamps": (None, [_P]),
+    # include/gguf_mmap.h (host only: the file mapping)
+    "gguf_mmap_open": (_P, [ctypes.c_char_p]),
+    "gguf_mmap_close": (None, [_P]),
+    "gguf_mmap_get_tensor": (_P, [_P, ctypes.c_char_p, ctypes.POINTER(_Z)]),
+    "gguf_get_tensor_ptr": (_P, [_P, ctypes.c_char_p, ctypes.POINTER(_Z)]),
+    "gguf_n_tensors": (_L, [_P]),
+    "gguf_tensor_name": (ctypes.c_char_p, [_P, _L]),
+    "gguf_tensor_type": (_I, [_P, _L]),
+    "gguf_tensor_ne": (ctypes.POINTER(ctypes.c_int64), [_P, _L]),
+    "gguf_tensor_dims": (ctypes.c_uint8, [_P, _L]),
+    "gguf_tensor_block_size": (_Z, [_P, _L]),
+    "gguf_tensor_type_size": (_Z, [_P, _L]),
+    "gguf_tensor_offset": (ctypes.c_uint64, [_P, _L]),
+    "gguf_tensor_nbytes": (_Z, [_P, _L]),
+    "gguf_n_kv": (_L, [_P]),
+    "gguf_kv_key": (ctypes.c_char_p, [_P, _L]),
+    "gguf_kv_type": (_I, [_P, _L]),
+    "gguf_kv_get_u8": (ctypes.c_int32, [_P, _L, ctypes.POINTER(ctypes.c_uint8)]),
+    "gguf_kv_get_i8": (ctypes.c_int32, [_P, _L, ctypes.POINTER(ctypes.c_int8)]),
+    "gguf_kv_get_u16": (ctypes.c_int32, [_P, _L, ctypes.POINTER(ctypes.c_uint16)]),
+    "gguf_kv_get_i16": (ctypes.c_int32, [_P, _L, ctypes.POINTER(ctypes.c_int16)]),
+    "gguf_kv_get_u32": (ctypes.c_int32, [_P, _L, ctypes.POINTER(ctypes.c_uint32)]),
+    "gguf_kv_get_i32": (ctypes.c_int32, [_P, _L, ctypes.POINTER(ctypes.c_int32)]),
+    "gguf_kv_get_f32": (ctypes.c_int32, [_P, _L, ctypes.POINTER(ctypes.c_float)]),
+    "gguf_kv_get_u64": (ctypes.c_int32, [_P, _L, ctypes.POINTER(ctypes.c_uint64)]),
+    "gguf_kv_get_i64": (ctypes.c_int32, [_P, _L, ctypes.POINTER(ctypes.c_int64)]),
+    "gguf_kv_get_f64": (ctypes.c_int32, [_P, _L, ctypes.POINTER(ctypes.c_double)]),
+    "gguf_alignment": (_Z, [_P]),
+    "gguf_data_offset": (_Z, [_P]),
+    "gguf_version": (ctypes.c_uint32, [_P]),
+    "gguf_arch": (ctypes.c_char_p, [_P]),
+    "gguf_block_count": (_L, [_P]),
+    "gguf_arch_int": (_L, [_P, ctypes.c_char_p, _L]),
+    "gguf_arch_float": (_F, [_P, ctypes.c_char_p, _F]),
+    "gguf_kv_str_val": (ctypes.c_char_p, [_P, _L]),
+    "gguf_find_kv": (_L, [_P, ctypes.c_char_p]),
+    "gguf_kv_get_array": (ctypes.c_int32, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int32),
+                                           ctypes.POINTER(_P), ctypes.POINTER(_Z)]),
+    "gguf_n_maps": (_I, [_P]),
+    "gguf_map_at": (_P, [_P, _I, ctypes.POINTER(_Z)]),
+    "gguf_last_error": (ctypes.c_char_p, []),
+    # include/moe_gguf.h
+    "moe_gguf_layer_bind": (_I, [_P, _I, _P]),
+    "moe_gguf_layer_upload": (_I, [_P, _I, _I, _P, _P]),
+    "moe_gguf_layer_release": (None, [_P]),
+    "moe_gguf_error": (ctypes.c_char_p, []),
 }
 
 
@@ -84,6 +130,11 @@ class LayerDesc(ctypes.Structure):
     _fields_ = [("type", _I), ("n_embd", _I), ("n_expert", _I), ("n_used", _I), ("n_ff", _I),
                 ("w_router", _P), ("w_gate", _P), ("w_up", _P), ("w_down", _P),
                 ("s_gate", _P), ("s_up", _P), ("s_down", _P), ("w_shexp", _P)]
+
+
+class GgufLayer(ctypes.Structure):
+    """struct moe_gguf_layer (include/moe_gguf.h)."""
+    _fields_ = [("desc", LayerDesc), ("dev", _P), ("dev_bytes", _Z), ("packed", _I)]
 
 
 class HipError(RuntimeError):
@@ -122,8 +173,10 @@ class MoeLib:
         def call(*args):
             r = fn(*args)
             if fn.restype is _I and name not in ("qmatvec_supported", "qmatvec_q8_supported", "qmatvec_id_batch_tile",
-                                                 "qmatvec_q8_id_batch_supported", "qmatvec_set_out_scale") and r != 0:
-                raise HipError(f"{name} returned hipError {r}")
+                                                 "qmatvec_q8_id_batch_supported", "qmatvec_set_out_scale") \
+                    and not name.startswith("gguf_") and r != 0:
+                why = f": {self.lib.moe_gguf_error().decode()}" if name.startswith("moe_gguf_") else ""
+                raise HipError(f"{name} returned {r}{why}")
             return r
         return call
 

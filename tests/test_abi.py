@@ -18,7 +18,8 @@ def declared_functions():
         src = open(h).read()
         src = re.sub(r"//[^\n]*", "", src)
         src = re.sub(r"static inline[^{]*\{.*?\n\}", "", src, flags=re.S)  # header-only helpers
-        for m in re.finditer(r"^(?:hipError_t|int|void|size_t)\s+\**\s*(\w+)\s*\(", src, flags=re.M):
+        for m in re.finditer(r"^(?:const\s+)?(?:hipError_t|int|void|size_t|int32_t|int64_t|uint8_t|uint32_t|uint64_t|float|char|"
+                             r"gguf_model_t)\s*\**\s*(\w+)\s*\(", src, flags=re.M):
             names.add(m.group(1))
     return names
 
