@@ -157,6 +157,73 @@ __global__ void __launch_bounds__(256) k_pack(const uint8_t* W, long long row_by
     }
 }
 
+// ------------------------------------------------------------------ MFMA operand tiles (prefill kernels)
+//
+// A second copy of a Q8_0 / ROCmFP4 / FAST matrix in the order the grouped MFMA kernel's lanes read it, so that
+// each of its 64-lane 16-byte loads is one contiguous 1 KB run (8 whole cache lines) instead of 64 pieces of
+// 64 rows. Per group of 32 rows g, in chunks of 1 KB, slot l (16 bytes) of a chunk for row 32 g + l % 32 and
+// K half h = l / 32 of a block:
+//   Q8_0:    chunk b = block b; the slot holds the block's int8 values 16 h .. 16 h + 15;
+//   ROCmFP4: chunk p = blocks 2p, 2p + 1; the slot holds 8 bytes of each: the block's nibble bytes 8 h .. 8 h + 7
+//            (low nibbles: values 8 h + i of the first 16-value half, high: values 16 + 8 h + i);
+//   FAST:    chunk p = blocks 2p, 2p + 1; 8 bytes of each: byte i = value 16 h + i | value 16 h + 8 + i << 4.
+// Scale tiles, per group g and 8-block group q: 32 row slots of 16 bytes (8 blocks' FP16 d, or UE4M3 e0 e1
+// pairs) or, for FAST, of 8 bytes (one e per block). A group's value tiles take 32 value-plane rows of bytes and
+// its scale tiles 32 scale-plane rows, so the tile copy is the size of the split-plane copy.
+__device__ __forceinline__ uint8_t fast_nibble(const uint8_t* qs, int v) {  // FAST value v (0..31) of a block
+    return v < 16 ? (qs[v] & 0x0f) : (qs[v - 16] >> 4);
+}
+
+template <int TYPE>
+__global__ void __launch_bounds__(256) k_pack_tiles(const uint8_t* W, long long row_bytes, long long rows, int K,
+                                                    uint8_t* V, uint8_t* S) {
+    constexpr int BB = Fmt<TYPE>::BLOCK_BYTES;
+    const int nb = K / 32, nch = TYPE == QT_Q8_0 ? nb : nb / 2;
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long nslots = rows / 32 * nch * 64;
+    if (i < nslots) {  // value slot (g, chunk c, lane l)
+        const int l = (int)(i & 63), h = l >> 5;
+        const long long gc = i >> 6, g = gc / nch;
+        const int c = (int)(gc - g * nch);
+        const uint8_t* row = W + (32 * g + (l & 31)) * row_bytes;
+        uint8_t out[16];
+        if constexpr (TYPE == QT_Q8_0) {
+            for (int j = 0; j < 16; ++j) out[j] = row[(long long)c * BB + 2 + 16 * h + j];
+        } else {
+            for (int k = 0; k < 2; ++k) {
+                const uint8_t* qs = row + (long long)(2 * c + k) * BB;
+                for (int j = 0; j < 8; ++j)
+                    out[8 * k + j] = TYPE == QT_ROCMFP4 ? qs[8 * h + j]
+                                                        : (uint8_t)(fast_nibble(qs, 16 * h + j) |
+                                                                    fast_nibble(qs, 16 * h + 8 + j) << 4);
+            }
+        }
+        uint8_t* dst = V + 16 * i;
+        for (int j = 0; j < 16; ++j) dst[j] = out[j];
+        return;
+    }
+    const long long k = i - nslots;  // scale slot (row r, 8-block group q)
+    const int nq = nb / 8;
+    if (k >= rows * nq) return;
+    const long long r = k / nq;
+    const int q = (int)(k - r * nq);
+    const uint8_t* row = W + r * row_bytes;
+    constexpr int SB = TYPE == QT_ROCMFP4_FAST ? 8 : 16;  // slot bytes
+    uint8_t* dst = S + ((r / 32) * nq + q) * (32 * SB) + (r & 31) * SB;
+    for (int b = 0; b < 8; ++b) {
+        const uint8_t* blk = row + (long long)(8 * q + b) * BB;
+        if constexpr (TYPE == QT_Q8_0) {
+            dst[2 * b] = blk[0];
+            dst[2 * b + 1] = blk[1];
+        } else if constexpr (TYPE == QT_ROCMFP4) {
+            dst[2 * b] = blk[16];
+            dst[2 * b + 1] = blk[17];
+        } else {
+            dst[b] = blk[16];
+        }
+    }
+}
+
 namespace {
 
 struct Packed {
@@ -164,8 +231,15 @@ struct Packed {
     int type, K;
     size_t row_bytes;
     long long rows;
-    uint8_t* mem;  // value plane, then scale plane
+    uint8_t* mem;    // value plane, then scale plane
+    uint8_t* tiles;  // MFMA operand tiles (value tiles, then scale tiles), or nullptr
 };
+
+// Whether a registered matrix also gets MFMA operand tiles: a type of the MFMA kernels, whole 32-row groups and
+// whole 8-block scale groups
+bool tiles_ok(int type, long long rows, int K) {
+    return (type == QT_Q8_0 || type == QT_ROCMFP4 || type == QT_ROCMFP4_FAST) && rows % 32 == 0 && K % 256 == 0;
+}
 
 std::mutex g_pack_mu;
 std::map<uintptr_t, Packed> g_packed;  // keyed by the native W's start address
@@ -193,6 +267,25 @@ bool find_packed(const void* W, int type, int K, size_t row_bytes, const uint8_t
     const long long row = (long long)(off / row_bytes);
     *v = p.mem + row * fmt_value_row(type, K);
     *s = p.mem + (size_t)p.rows * fmt_value_row(type, K) + row * fmt_scale_row(type, K);
+    return true;
+}
+
+// The MFMA operand tiles of the registered matrix whose native rows start at W (at a 32-row group boundary): the
+// value tiles and scale tiles of W's first row group, or false
+bool find_tiles(const void* W, int type, int K, size_t row_bytes, const uint8_t** vt, const uint8_t** st) {
+    if (!W) return false;
+    std::lock_guard<std::mutex> lk(g_pack_mu);
+    auto it = g_packed.upper_bound((uintptr_t)W);
+    if (it == g_packed.begin()) return false;
+    --it;
+    const Packed& p = it->second;
+    const uintptr_t off = (uintptr_t)W - it->first;
+    if ((uintptr_t)W >= p.end || !p.tiles || p.type != type || p.K != K || p.row_bytes != row_bytes ||
+        off % (32 * row_bytes))
+        return false;
+    const long long g = (long long)(off / (32 * row_bytes));
+    *vt = p.tiles + g * 32 * fmt_value_row(type, K);
+    *st = p.tiles + (size_t)p.rows * fmt_value_row(type, K) + g * 32 * fmt_scale_row(type, K);
     return true;
 }
 
@@ -319,14 +412,29 @@ extern "C" size_t qmatvec_packed_bytes(int type, long long rows, int K) {
     return rows > 0 ? rb * (size_t)rows : 0;
 }
 
+// Bytes of the split-plane copy (value plane + scale plane); the tile copy, when made, is the same size
+static size_t packed_planes_bytes(int type, long long rows, int K) {
+    return (size_t)rows * (size_t)(fmt_value_row(type, K) + fmt_scale_row(type, K));
+}
+
 template <int TYPE>
-static hipError_t launch_pack(const void* W, size_t rb, long long rows, int K, uint8_t* mem, hipStream_t st) {
+static hipError_t launch_pack(const void* W, size_t rb, long long rows, int K, uint8_t* mem, uint8_t* tiles,
+                              hipStream_t st) {
     constexpr int BV = TYPE == QT_Q4_K ? 256 : 32;
     const long long n = rows * (K / BV);
     uint8_t* V = mem;
     uint8_t* S = mem + (size_t)rows * fmt_value_row(TYPE, K);
-    return launch_kernel(k_pack<TYPE>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const uint8_t*)W,
-                         (long long)rb, rows, K, V, S);
+    hipError_t e = launch_kernel(k_pack<TYPE>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                                 (const uint8_t*)W, (long long)rb, rows, K, V, S);
+    if constexpr (TYPE != QT_Q4_K) {
+        if (e == hipSuccess && tiles) {
+            const long long nt = rows / 32 * (TYPE == QT_Q8_0 ? K / 32 : K / 64) * 64 + rows * (K / 256);
+            e = launch_kernel(k_pack_tiles<TYPE>, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st,
+                              (const uint8_t*)W, (long long)rb, rows, K, tiles,
+                              tiles + (size_t)rows * fmt_value_row(TYPE, K));
+        }
+    }
+    return e;
 }
 
 extern "C" hipError_t qmatvec_pack_weights(int type, const void* W, size_t row_bytes, long long rows, int K,
@@ -341,21 +449,25 @@ extern "C" hipError_t qmatvec_pack_weights(int type, const void* W, size_t row_b
         if (it != g_packed.end() && it->first < (uintptr_t)W + bytes) return hipErrorInvalidValue;  // overlap
         if (it != g_packed.begin() && std::prev(it)->second.end > (uintptr_t)W) return hipErrorInvalidValue;
     }
+    const size_t planes = packed_planes_bytes(type, rows, K);
+    const bool tiled = tiles_ok(type, rows, K);
     void* mem = nullptr;
-    hipError_t e = hipMalloc(&mem, bytes);
+    hipError_t e = hipMalloc(&mem, tiled ? 2 * planes : planes);
     if (e != hipSuccess) return e;
+    uint8_t* m8 = (uint8_t*)mem;
+    uint8_t* tiles = tiled ? m8 + planes : nullptr;
     switch (type) {
-    case QT_Q8_0: e = launch_pack<QT_Q8_0>(W, row_bytes, rows, K, (uint8_t*)mem, stream); break;
-    case QT_ROCMFP4: e = launch_pack<QT_ROCMFP4>(W, row_bytes, rows, K, (uint8_t*)mem, stream); break;
-    case QT_ROCMFP4_FAST: e = launch_pack<QT_ROCMFP4_FAST>(W, row_bytes, rows, K, (uint8_t*)mem, stream); break;
-    default: e = launch_pack<QT_Q4_K>(W, row_bytes, rows, K, (uint8_t*)mem, stream); break;
+    case QT_Q8_0: e = launch_pack<QT_Q8_0>(W, row_bytes, rows, K, m8, tiles, stream); break;
+    case QT_ROCMFP4: e = launch_pack<QT_ROCMFP4>(W, row_bytes, rows, K, m8, tiles, stream); break;
+    case QT_ROCMFP4_FAST: e = launch_pack<QT_ROCMFP4_FAST>(W, row_bytes, rows, K, m8, tiles, stream); break;
+    default: e = launch_pack<QT_Q4_K>(W, row_bytes, rows, K, m8, nullptr, stream); break;
     }
     if (e != hipSuccess) {
         (void)hipFree(mem);
         return e;
     }
     std::lock_guard<std::mutex> lk(g_pack_mu);
-    g_packed[(uintptr_t)W] = Packed{(uintptr_t)W + bytes, type, K, row_bytes, rows, (uint8_t*)mem};
+    g_packed[(uintptr_t)W] = Packed{(uintptr_t)W + bytes, type, K, row_bytes, rows, m8, tiles};
     return hipSuccess;
 }
 
@@ -382,6 +494,11 @@ void moe_mv_shape(int type, int K, int* lanes, int* units_per_lane) {
 // The split-plane rows of the registered matrix at W (for the fused layer kernel)
 bool moe_packed_planes(const void* W, int type, int K, size_t row_bytes, const uint8_t** v, const uint8_t** s) {
     return find_packed(W, type, K, row_bytes, v, s);
+}
+
+// The MFMA operand tiles of the registered matrix at W (for the layer's grouped launches)
+bool moe_packed_tiles(const void* W, int type, int K, size_t row_bytes, const uint8_t** vt, const uint8_t** st) {
+    return find_tiles(W, type, K, row_bytes, vt, st);
 }
 
 // Drop every registration (library teardown)
@@ -493,9 +610,9 @@ extern "C" hipError_t qmatvec_launch_q8_batch(int type, const void* W, size_t ro
                                               long long ldy, int N, int K, int T, hipStream_t stream) {
     const uint8_t *v = nullptr, *s = nullptr;
     if (T >= DENSE_MFMA_MIN_T && N > 0 && ldy >= N && y && check_common(type, W, row_bytes, q, K, T) == hipSuccess &&
-        moe_grouped_mfma_ok(type, N, K) && find_packed(W, type, K, row_bytes, &v, &s))
-        return moe_launch_dense_mfma(type, v, s, fmt_value_row(type, K), fmt_scale_row(type, K), q, y, ldy, N, K, T,
-                                     stream);
+        moe_grouped_mfma_ok(type, N, K) && find_tiles(W, type, K, row_bytes, &v, &s))
+        return moe_launch_dense_mfma(type, v, s, 32 * fmt_value_row(type, K), 32 * fmt_scale_row(type, K), q, y, ldy,
+                                     N, K, T, stream);
     return dense(type, W, N, y, nullptr, 0, nullptr, row_bytes, q, K, T, ldy, stream);
 }
 
@@ -558,8 +675,8 @@ extern "C" hipError_t qmatvec_launch_q8_id_batch(int type, const void* W, size_t
     if (!qmatvec_q8_supported(type, K)) return hipErrorInvalidDeviceFunction;
     if (!W || !q || row_bytes != native_row(type, K) || !aligned(W, 4)) return hipErrorInvalidValue;
     const uint8_t *v = nullptr, *s = nullptr;
-    if (moe_grouped_mfma_ok(type, N, K) && find_packed(W, type, K, row_bytes, &v, &s))
-        return moe_launch_grouped_mfma(type, v, s, fmt_value_row(type, K), fmt_scale_row(type, K), q, y, N, K,
+    if (moe_grouped_mfma_ok(type, N, K) && find_tiles(W, type, K, row_bytes, &v, &s))
+        return moe_launch_grouped_mfma(type, v, s, 32 * fmt_value_row(type, K), 32 * fmt_scale_row(type, K), q, y, N, K,
                                        max_tiles, n_tiles, tile_e, tile_start, tile_n, in_rows, out_rows, stream);
     return moe_launch_entries(type, W, row_bytes, q, y, N, K, max_tiles, n_tiles, tile_e, tile_start, tile_n, in_rows,
                               out_rows, stream);

@@ -30,9 +30,9 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 struct GArgs {
-    const uint8_t* v;  // value plane of the stacked experts
-    const uint8_t* s;  // scale plane
-    long long vrb, srb;
+    const uint8_t* v;  // value tiles of the stacked experts' first 32-row group (MFMA operand tiles)
+    const uint8_t* s;  // scale tiles
+    long long vrb, srb;  // bytes of value / scale tiles per 32-row group
     const int8_t* xq;  // Q8_0 activation values, rows of K
     const float* xd;   // Q8_0 activation scales, rows of K / 32
     float* y;
@@ -45,7 +45,7 @@ struct GArgs {
     const int* out_rows;  // nullptr: entry i writes output row tile_start + i
     long long ldy;        // output row stride
     int T;                // n_tiles == nullptr (dense): T rows of one matrix in tiles of GG_TILE
-    const uint8_t* v2;    // the up matrix's planes (gate / up / SwiGLU kernel)
+    const uint8_t* v2;    // the up matrix's tiles (gate / up / SwiGLU kernel)
     const uint8_t* s2;
     int8_t* aq;           // SwiGLU kernel: down's Q8_0 input, rows of N values (out_rows), and scales
     float* ad;
@@ -87,9 +87,16 @@ __device__ __forceinline__ void acc_block(v16f& acc, const v16i& I, const v16f& 
 // The weight rows' scale bytes come through registers.
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <int NM, int KB>
+// Weight chunks of 1 KB per stage of KB blocks: one per block (Q8_0), one per block pair (FP4 types)
+template <int TYPE, int KB>
+struct GChunks {
+    static constexpr int PER = TYPE == QT_Q8_0 ? 1 : 2;
+    static constexpr int N = KB / PER;
+};
+
+template <int TYPE, int NM, int KB>
 struct GBuf {  // one stage of operands of NM weight matrices sharing the activations
-    uint8_t a[NM][4][KB][1024];     // [matrix][wave][block][lane * 16]
+    uint8_t a[NM][4][GChunks<TYPE, KB>::N][1024];  // [matrix][wave][chunk][lane * 16]
     uint8_t b[KB][GG_NT][1024];     // [block][entry tile][lane * 16]
     float dx[KB / 4][GG_TILE][4];   // [block / 4][entry][block % 4]
 };
@@ -108,18 +115,15 @@ __device__ __forceinline__ void wait_vm() {
 // activations of entry tile w % GG_NT, blocks w / GG_NT, + 4 / GG_NT, ... (xrow: its lane's entry row), and the
 // scales of entries GG_TILE / 4 w .. (dxr: its lane's entry row)
 template <int TYPE, int NM, int KB>
-__device__ __forceinline__ void g_issue(GBuf<NM, KB>& B, int b0, uint4 (&wsc)[NM], const uint8_t* const (&vrow)[NM],
-                                        const uint8_t* const (&srow)[NM], const int8_t* xrow, const float* dxr, int nb,
-                                        int w, int l, int kh) {
+__device__ __forceinline__ void g_issue(GBuf<TYPE, NM, KB>& B, int b0, uint4 (&wsc)[NM],
+                                        const uint8_t* const (&vt)[NM], const uint8_t* const (&st)[NM],
+                                        const int8_t* xrow, const float* dxr, int w, int l) {
     constexpr int ES = GG_TILE / 4;  // entries whose scales one wave loads
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int bb = 0; bb < KB; ++bb) {
-            const uint8_t* g =
-                TYPE == QT_Q8_0 ? vrow[m] + 16 * (kh ? nb + b0 + bb : b0 + bb) : vrow[m] + 16 * (b0 + bb);
-            lds_load16(g, B.a[m][w][bb]);
-        }
+        for (int c = 0; c < GChunks<TYPE, KB>::N; ++c)  // contiguous 1 KB chunks: one per block, or block pair
+            lds_load16(vt[m] + 1024 * (b0 / GChunks<TYPE, KB>::PER + c), B.a[m][w][c]);
 #pragma unroll
     for (int j = 0; j < KB * GG_NT / 4; ++j) {
         const int bb = w / GG_NT + (4 / GG_NT) * j;
@@ -129,18 +133,20 @@ __device__ __forceinline__ void g_issue(GBuf<NM, KB>& B, int b0, uint4 (&wsc)[NM
     for (int q = 0; q < KB / 4; ++q)
         if (l < ES) lds_load16(dxr + b0 + 4 * q, &B.dx[q][ES * w][0]);  // (lanes ES.. idle)
 #pragma unroll
-    for (int m = 0; m < NM; ++m) {
-        if constexpr (TYPE == QT_ROCMFP4_FAST) {  // 1 scale byte per block
+    for (int m = 0; m < NM; ++m) {  // the lane's row's slot of the stage's 8-block scale group
+        if constexpr (TYPE == QT_ROCMFP4_FAST) {  // 1 scale byte per block, 8-byte slots
+            const uint8_t* g = st[m] + 256 * (b0 >> 3);
             if constexpr (KB == 4)
-                wsc[m] = make_uint4(*(const uint32_t*)(srow[m] + b0), 0u, 0u, 0u);
+                wsc[m] = make_uint4(*(const uint32_t*)(g + 4 * ((b0 >> 2) & 1)), 0u, 0u, 0u);
             else
-                wsc[m] = make_uint4(((const uint2*)(srow[m] + b0))->x, ((const uint2*)(srow[m] + b0))->y, 0u, 0u);
-        } else {  // 2 scale bytes per block
+                wsc[m] = make_uint4(((const uint2*)g)->x, ((const uint2*)g)->y, 0u, 0u);
+        } else {  // 2 scale bytes per block, 16-byte slots
+            const uint8_t* g = st[m] + 512 * (b0 >> 3);
             if constexpr (KB == 4) {
-                const uint2 v = *(const uint2*)(srow[m] + 2 * b0);
+                const uint2 v = *(const uint2*)(g + 8 * ((b0 >> 2) & 1));
                 wsc[m] = make_uint4(v.x, v.y, 0u, 0u);
             } else {
-                wsc[m] = *(const uint4*)(srow[m] + 2 * b0);
+                wsc[m] = *(const uint4*)g;
             }
         }
     }
@@ -148,7 +154,7 @@ __device__ __forceinline__ void g_issue(GBuf<NM, KB>& B, int b0, uint4 (&wsc)[NM
 
 // The MFMAs of one stage from B
 template <int TYPE, int NM, int KB>
-__device__ __forceinline__ void g_compute(const GBuf<NM, KB>& B, const uint4 (&wsc)[NM], v16f (&acc)[NM][GG_NT], int w,
+__device__ __forceinline__ void g_compute(const GBuf<TYPE, NM, KB>& B, const uint4 (&wsc)[NM], v16f (&acc)[NM][GG_NT], int w,
                                           int l, int lr, int kh) {
     const v16i zi = {};
 #pragma unroll
@@ -160,9 +166,10 @@ __device__ __forceinline__ void g_compute(const GBuf<NM, KB>& B, const uint4 (&w
         for (int m = 0; m < NM; ++m) {
             const uint32_t w2 = bb < 2 ? wsc[m].x : bb < 4 ? wsc[m].y : bb < 6 ? wsc[m].z : wsc[m].w;  // 2-byte
             const uint32_t w1 = bb < 4 ? wsc[m].x : wsc[m].y;                                        // 1-byte
-            const uint8_t* arun = B.a[m][w][bb] + 16 * l;
+            // the lane's slot: 16 bytes of block bb (Q8_0), or 8 bytes of block bb in its pair's slot (FP4 types)
+            const uint8_t* arun = TYPE == QT_Q8_0 ? B.a[m][w][bb] + 16 * l : B.a[m][w][bb >> 1] + 16 * l + 8 * (bb & 1);
             if constexpr (TYPE == QT_ROCMFP4) {
-                const uint2 q = *(const uint2*)(arun + 8 * kh);  // bytes 8 kh .. 8 kh + 7 of the row's block
+                const uint2 q = *(const uint2*)arun;  // nibble bytes 8 kh .. 8 kh + 7 of the row's block
                 const uint32_t ew = w2 >> (16 * (bb & 1));
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
@@ -180,16 +187,16 @@ __device__ __forceinline__ void g_compute(const GBuf<NM, KB>& B, const uint4 (&w
                     }
                 }
             } else {
-                const uint4 q = *(const uint4*)arun;
                 v4i A;
                 float dw;
                 if constexpr (TYPE == QT_Q8_0) {
+                    const uint4 q = *(const uint4*)arun;
                     A = (v4i){(int)q.x, (int)q.y, (int)q.z, (int)q.w};
                     dw = h2f((uint16_t)(w2 >> (16 * (bb & 1))));
-                } else {  // FAST: K half kh = the low (0) or high (1) nibbles of the block's 16 bytes
-                    const uint32_t sh = kh ? 4 : 0;
-                    A = (v4i){(int)fp4x4_to_i8x4(q.x >> sh), (int)fp4x4_to_i8x4(q.y >> sh),
-                              (int)fp4x4_to_i8x4(q.z >> sh), (int)fp4x4_to_i8x4(q.w >> sh)};
+                } else {  // FAST: K half kh's 16 values, value i and i + 8 in byte i's low and high nibble
+                    const uint2 q = *(const uint2*)arun;
+                    A = (v4i){(int)fp4x4_to_i8x4(q.x), (int)fp4x4_to_i8x4(q.y), (int)fp4x4_to_i8x4(q.x >> 4),
+                              (int)fp4x4_to_i8x4(q.y >> 4)};
                     dw = ue4m3_half((w1 >> (8 * (bb & 3))) & 0xffu);
                 }
 #pragma unroll
@@ -209,7 +216,7 @@ __device__ __forceinline__ void g_compute(const GBuf<NM, KB>& B, const uint4 (&w
 // block: 16 values in each of lanes l and l + 32 -- into a.aq / a.ad (the quantizer's expressions).
 template <int TYPE, int NM, int KB>
 __global__ void __launch_bounds__(256) k_grouped(GArgs a) {
-    __shared__ __attribute__((aligned(1024))) GBuf<NM, KB> buf;
+    __shared__ __attribute__((aligned(1024))) GBuf<TYPE, NM, KB> buf;
     const int k = blockIdx.y;
     int e, st, cnt;
     if (a.n_tiles) {
@@ -227,16 +234,18 @@ __global__ void __launch_bounds__(256) k_grouped(GArgs a) {
     auto in_row = [&](int i) { return a.in_rows ? a.in_rows[st + i] : st + i; };
     auto out_row = [&](int i) { return a.out_rows ? a.out_rows[st + i] : st + i; };
     const int K = a.K, nb = K / 32;
-    // this lane's weight row (the launcher requires N % 128 == 0 and K % (32 KB) == 0)
+    // the wave's 32-row group of the stacked matrix (the launcher requires N % 128 == 0 and K % 256 == 0) and
+    // this lane's slots in its value and scale tiles
     const int r0 = blockIdx.x * GG_ROWS + 32 * w;
-    const long long grow = (long long)e * a.N + r0 + lr;
-    const uint8_t* vrow[NM];
-    const uint8_t* srow[NM];
-    vrow[0] = a.v + grow * a.vrb;
-    srow[0] = a.s + grow * a.srb;
+    const long long grp = ((long long)e * a.N + r0) / 32;
+    constexpr int SB = TYPE == QT_ROCMFP4_FAST ? 8 : 16;
+    const uint8_t* vt[NM];
+    const uint8_t* sct[NM];
+    vt[0] = a.v + grp * a.vrb + 16 * l;
+    sct[0] = a.s + grp * a.srb + SB * lr;
     if constexpr (NM == 2) {
-        vrow[1] = a.v2 + grow * a.vrb;
-        srow[1] = a.s2 + grow * a.srb;
+        vt[1] = a.v2 + grp * a.vrb + 16 * l;
+        sct[1] = a.s2 + grp * a.srb + SB * lr;
     }
     // the entry rows this lane loads: activations of entry 32 (w % GG_NT) + lr, scales of entry GG_TILE / 4 w + l
     const int8_t* xrow = a.xq + (long long)in_row(min(32 * (w % GG_NT) + lr, cnt - 1)) * K + 16 * kh;
@@ -252,7 +261,7 @@ __global__ void __launch_bounds__(256) k_grouped(GArgs a) {
     for (int s = 0; s < nst; ++s) {
         // one stage: its loads, then (with several workgroups per CU hiding the latency of each other's loads)
         // its MFMAs
-        g_issue<TYPE, NM, KB>(buf, s * KB, wsc, vrow, srow, xrow, dxr, nb, w, l, kh);
+        g_issue<TYPE, NM, KB>(buf, s * KB, wsc, vt, sct, xrow, dxr, w, l);
         wait_vm<0>();
         __syncthreads();
         g_compute<TYPE, NM, KB>(buf, wsc, acc, w, l, lr, kh);

@@ -19,7 +19,7 @@ bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits,
 bool moe_fused_multi_try(const moe_layer_desc* d, const float* x, const float* logits, int T, float* out,
                          int* ids_out, float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err);
 
-bool moe_packed_planes(const void* W, int type, int K, size_t row_bytes, const uint8_t** v, const uint8_t** s);
+bool moe_packed_tiles(const void* W, int type, int K, size_t row_bytes, const uint8_t** vt, const uint8_t** st);
 bool moe_grouped_mfma_ok(int type, int N, int K);
 hipError_t moe_launch_grouped_swiglu(int type, const uint8_t* vg, const uint8_t* sg, const uint8_t* vu,
                                      const uint8_t* su, long long vrb, long long srb, const qmatvec_q8* q, int8_t* aq,
@@ -192,11 +192,12 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
                                gpu_moe_group_ws_bytes(T, NE), st));
         const uint8_t *vg = nullptr, *sgp = nullptr, *vu = nullptr, *sup = nullptr, *vd = nullptr, *sdp = nullptr;
         if (mode && moe_grouped_mfma_ok(type, FE, E) && moe_grouped_mfma_ok(type, E, FE) &&
-            moe_packed_planes(d->w_gate, type, E, rb_in, &vg, &sgp) &&
-            moe_packed_planes(d->w_up, type, E, rb_in, &vu, &sup) &&
-            moe_packed_planes(d->w_down, type, FE, rb_out, &vd, &sdp)) {
+            moe_packed_tiles(d->w_gate, type, E, rb_in, &vg, &sgp) &&
+            moe_packed_tiles(d->w_up, type, E, rb_in, &vu, &sup) &&
+            moe_packed_tiles(d->w_down, type, FE, rb_out, &vd, &sdp)) {
             // gate, up, SwiGLU and down's Q8_0 input in one launch (the same bits as the three launches below)
-            CHECK(moe_launch_grouped_swiglu(type, vg, sgp, vu, sup, value_row(type, E), scale_row(type, E), &qx, qa.q0,
+            CHECK(moe_launch_grouped_swiglu(type, vg, sgp, vu, sup, 32 * value_row(type, E), 32 * scale_row(type, E),
+                                            &qx, qa.q0,
                                             qa.d0, FE, E, p.max_tiles, ntile, te, ts, tn, tok, pair, st));
         } else {
             CHECK(qmatvec_launch_q8_id_batch(type, d->w_gate, rb_in, &qx, g, FE, E, p.max_tiles, p.tile, ntile, te,
