@@ -622,7 +622,7 @@ extern "C" hipError_t qmatvec_launch_q8_batch(int type, const void* W, size_t ro
 hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
                                    const qmatvec_q8* q, float* y, int N, int K, int max_tiles, const int32_t* n_tiles,
                                    const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
-                                   const int32_t* in_rows, const int32_t* out_rows, hipStream_t stream);
+                                   const int32_t* in_rows, const int32_t* out_rows, int xt, hipStream_t stream);
 
 hipError_t moe_launch_entries(int type, const void* W, size_t row_bytes, const qmatvec_q8* q, float* y, int N, int K,
                               int max_tiles, const int32_t* n_tiles, const int32_t* tile_e, const int32_t* tile_start,
@@ -677,7 +677,7 @@ extern "C" hipError_t qmatvec_launch_q8_id_batch(int type, const void* W, size_t
     const uint8_t *v = nullptr, *s = nullptr;
     if (moe_grouped_mfma_ok(type, N, K) && find_tiles(W, type, K, row_bytes, &v, &s))
         return moe_launch_grouped_mfma(type, v, s, 32 * fmt_value_row(type, K), 32 * fmt_scale_row(type, K), q, y, N, K,
-                                       max_tiles, n_tiles, tile_e, tile_start, tile_n, in_rows, out_rows, stream);
+                                       max_tiles, n_tiles, tile_e, tile_start, tile_n, in_rows, out_rows, 0, stream);
     return moe_launch_entries(type, W, row_bytes, q, y, N, K, max_tiles, n_tiles, tile_e, tile_start, tile_n, in_rows,
                               out_rows, stream);
 }

@@ -49,7 +49,16 @@ struct GArgs {
     const uint8_t* s2;
     int8_t* aq;           // SwiGLU kernel: down's Q8_0 input, rows of N values (out_rows), and scales
     float* ad;
+    int xt;               // GX_IN: the input activations are in entry-tile order (below) instead of rows;
+                          // GX_OUT: the SwiGLU kernel writes down's input in entry-tile order
 };
+#define GX_IN 1
+#define GX_OUT 2
+
+// Entry-tile order of a Q8_0 activation matrix of K values per entry: tile k's values at xq + k * GG_TILE * K, in
+// 1 KB chunks (block b, 32-entry sub-tile t) at ((b * GG_NT + t) * 1024; slot l (16 bytes) of a chunk holds entry
+// 32 t + l % 32, values 16 (l / 32) .. + 15 of the block: one contiguous run per 64-lane MFMA operand load. The
+// scales are rows: entry i of tile k at xd + (k * GG_TILE + i) * K / 32.
 
 #define GG_ROWS 128  // weight rows per workgroup (32 per wave)
 #ifndef GG_TILE
@@ -117,7 +126,7 @@ __device__ __forceinline__ void wait_vm() {
 template <int TYPE, int NM, int KB>
 __device__ __forceinline__ void g_issue(GBuf<TYPE, NM, KB>& B, int b0, uint4 (&wsc)[NM],
                                         const uint8_t* const (&vt)[NM], const uint8_t* const (&st)[NM],
-                                        const int8_t* xrow, const float* dxr, int w, int l) {
+                                        const int8_t* xrow, int xs, const float* dxr, int w, int l) {
     constexpr int ES = GG_TILE / 4;  // entries whose scales one wave loads
 #pragma unroll
     for (int m = 0; m < NM; ++m)
@@ -127,7 +136,7 @@ __device__ __forceinline__ void g_issue(GBuf<TYPE, NM, KB>& B, int b0, uint4 (&w
 #pragma unroll
     for (int j = 0; j < KB * GG_NT / 4; ++j) {
         const int bb = w / GG_NT + (4 / GG_NT) * j;
-        lds_load16(xrow + 32 * (b0 + bb), B.b[bb][w % GG_NT]);
+        lds_load16(xrow + xs * (b0 + bb), B.b[bb][w % GG_NT]);
     }
 #pragma unroll
     for (int q = 0; q < KB / 4; ++q)
@@ -248,8 +257,19 @@ __global__ void __launch_bounds__(256) k_grouped(GArgs a) {
         sct[1] = a.s2 + grp * a.srb + SB * lr;
     }
     // the entry rows this lane loads: activations of entry 32 (w % GG_NT) + lr, scales of entry GG_TILE / 4 w + l
-    const int8_t* xrow = a.xq + (long long)in_row(min(32 * (w % GG_NT) + lr, cnt - 1)) * K + 16 * kh;
-    const float* dxr = a.xd + (long long)in_row(min(GG_TILE / 4 * w + (l & (GG_TILE / 4 - 1)), cnt - 1)) * nb;
+    const int de = min(GG_TILE / 4 * w + (l & (GG_TILE / 4 - 1)), cnt - 1);  // the entry whose scales this lane loads
+    const int8_t* xrow;
+    const float* dxr;
+    int xs;  // bytes from one block's operand run to the next
+    if (a.xt & GX_IN) {
+        xrow = a.xq + ((long long)k * nb * GG_NT + w % GG_NT) * 1024 + 16 * l;
+        xs = GG_NT * 1024;
+        dxr = a.xd + ((long long)k * GG_TILE + de) * nb;
+    } else {
+        xrow = a.xq + (long long)in_row(min(32 * (w % GG_NT) + lr, cnt - 1)) * K + 16 * kh;
+        xs = 32;
+        dxr = a.xd + (long long)in_row(de) * nb;
+    }
 
     v16f acc[NM][GG_NT];
 #pragma unroll
@@ -261,7 +281,7 @@ __global__ void __launch_bounds__(256) k_grouped(GArgs a) {
     for (int s = 0; s < nst; ++s) {
         // one stage: its loads, then (with several workgroups per CU hiding the latency of each other's loads)
         // its MFMAs
-        g_issue<TYPE, NM, KB>(buf, s * KB, wsc, vt, sct, xrow, dxr, w, l);
+        g_issue<TYPE, NM, KB>(buf, s * KB, wsc, vt, sct, xrow, xs, dxr, w, l);
         wait_vm<0>();
         __syncthreads();
         g_compute<TYPE, NM, KB>(buf, wsc, acc, w, l, lr, kh);
@@ -290,14 +310,18 @@ __global__ void __launch_bounds__(256) k_grouped(GArgs a) {
             am = fmaxf(am, __shfl_xor(am, 32, 64));  // the block's other 16 rows
             const float id = am != 0.0f ? 127.0f / am : 0.0f;
             if (32 * t + lr < cnt) {
-                const long long pr = out_row(32 * t + lr);
-                int8_t* q = a.aq + pr * a.N + r0;
+                // entry-tile order: block r0 / 32 of entry 32 t + lr; else the entry's output row
+                const bool xo = a.xt & GX_OUT;
+                const long long pr = xo ? (long long)k * GG_TILE + 32 * t + lr : out_row(32 * t + lr);
+                int8_t* q = xo ? a.aq + (((long long)k * (a.N / 32) + r0 / 32) * GG_NT + t) * 1024 + 16 * lr
+                                 : a.aq + pr * a.N + r0;
 #pragma unroll
                 for (int m4 = 0; m4 < 4; ++m4) {  // rows 8 m4 + 4 kh .. + 3: four consecutive bytes
                     uint32_t pk = 0;
 #pragma unroll
                     for (int c = 0; c < 4; ++c) pk |= ((uint32_t)(int)rintf(act[4 * m4 + c] * id) & 0xffu) << (8 * c);
-                    *(uint32_t*)(q + 8 * m4 + 4 * kh) = pk;
+                    const int row = 8 * m4 + 4 * kh;  // of the block: K half row / 16, byte row % 16 of it
+                    *(uint32_t*)(q + (xo ? 512 * (row >> 4) + (row & 15) : row)) = pk;
                 }
                 if (kh == 0) a.ad[pr * (a.N / 32) + r0 / 32] = __half2float(__float2half(am / 127.0f));
             }
@@ -318,9 +342,9 @@ int moe_grouped_mfma_tile(void) { return GG_TILE; }
 hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
                                    const qmatvec_q8* q, float* y, int N, int K, int max_tiles, const int32_t* n_tiles,
                                    const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
-                                   const int32_t* in_rows, const int32_t* out_rows, hipStream_t stream) {
+                                   const int32_t* in_rows, const int32_t* out_rows, int xt, hipStream_t stream) {
     GArgs a = {v,      s,       vrb,      srb, q->q0, q->d0, y,       N,       K,       n_tiles, tile_e,
-               tile_start, tile_n, in_rows, out_rows, N, 0, nullptr, nullptr, nullptr, nullptr};
+               tile_start, tile_n, in_rows, out_rows, N, 0, nullptr, nullptr, nullptr, nullptr, xt};
     const dim3 g(N / GG_ROWS, max_tiles), b(256);
     switch (type) {
     case QT_Q8_0: return launch_kernel(k_grouped<QT_Q8_0, 1, GG_KB>, g, b, 0, stream, a);
@@ -330,15 +354,15 @@ hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s,
     return hipErrorInvalidDeviceFunction;
 }
 
-// Gate and up of the same tiles in one launch, then SwiGLU and down's Q8_0 input (aq rows of N, ad per 32)
-// instead of the gate / up outputs
+// Gate and up of the same tiles in one launch, then SwiGLU and down's Q8_0 input (aq rows of N, ad per 32; in
+// entry-tile order with xt = GX_OUT) instead of the gate / up outputs. xt: GX_IN / GX_OUT flags (GArgs::xt)
 hipError_t moe_launch_grouped_swiglu(int type, const uint8_t* vg, const uint8_t* sg, const uint8_t* vu,
                                      const uint8_t* su, long long vrb, long long srb, const qmatvec_q8* q, int8_t* aq,
                                      float* ad, int N, int K, int max_tiles, const int32_t* n_tiles,
                                      const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
-                                     const int32_t* in_rows, const int32_t* out_rows, hipStream_t stream) {
+                                     const int32_t* in_rows, const int32_t* out_rows, int xt, hipStream_t stream) {
     GArgs a = {vg,         sg,     vrb,     srb,      q->q0, q->d0, nullptr, N,  K,  n_tiles, tile_e,
-               tile_start, tile_n, in_rows, out_rows, N,     0,     vu,      su, aq, ad};
+               tile_start, tile_n, in_rows, out_rows, N,     0,     vu,      su, aq, ad, xt};
     const dim3 g(N / GG_ROWS, max_tiles), b(256);
     switch (type) {
     case QT_Q8_0: return launch_kernel(k_grouped<QT_Q8_0, 2, GG_KB2>, g, b, 0, stream, a);
@@ -353,7 +377,7 @@ hipError_t moe_launch_dense_mfma(int type, const uint8_t* v, const uint8_t* s, l
                                  const qmatvec_q8* q, float* y, long long ldy, int N, int K, int T,
                                  hipStream_t stream) {
     GArgs a = {v,       s,       vrb,     srb,     q->q0, q->d0, y,       N,       K,       nullptr, nullptr,
-               nullptr, nullptr, nullptr, nullptr, ldy,   T,     nullptr, nullptr, nullptr, nullptr};
+               nullptr, nullptr, nullptr, nullptr, ldy,   T,     nullptr, nullptr, nullptr, nullptr, 0};
     const dim3 g(N / GG_ROWS, (T + GG_TILE - 1) / GG_TILE), b(256);
     switch (type) {
     case QT_Q8_0: return launch_kernel(k_grouped<QT_Q8_0, 1, GG_KB>, g, b, 0, stream, a);

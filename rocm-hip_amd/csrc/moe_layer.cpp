@@ -5,6 +5,7 @@
 
 #include <stdint.h>
 
+#include <algorithm>
 #include <atomic>
 
 #include "gpu_ops.h"
@@ -25,7 +26,11 @@ hipError_t moe_launch_grouped_swiglu(int type, const uint8_t* vg, const uint8_t*
                                      const uint8_t* su, long long vrb, long long srb, const qmatvec_q8* q, int8_t* aq,
                                      float* ad, int N, int K, int max_tiles, const int32_t* n_tiles,
                                      const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
-                                     const int32_t* in_rows, const int32_t* out_rows, hipStream_t stream);
+                                     const int32_t* in_rows, const int32_t* out_rows, int xt, hipStream_t stream);
+hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
+                                   const qmatvec_q8* q, float* y, int N, int K, int max_tiles, const int32_t* n_tiles,
+                                   const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
+                                   const int32_t* in_rows, const int32_t* out_rows, int xt, hipStream_t stream);
 
 hipError_t moe_quantize_q8_0(const float* x, int n, const qmatvec_q8* q, hipStream_t stream);
 
@@ -69,7 +74,8 @@ Plan plan(const moe_layer_desc* d, int T) {
     p.fused = moe_fused_scratch_bytes(d, T < FUSED_MAX_T ? T : FUSED_MAX_T);
     p.max_tiles = gpu_moe_max_tiles(T, NU, NE, p.tile);
     p.qx_k = r256((long long)T * E);
-    p.qa_k = r256((long long)T * p.NS * FE);
+    // down's input: pair rows, or (the fused prefill) entry tiles of p.tile rows each
+    p.qa_k = r256(std::max((long long)T * p.NS, (long long)p.max_tiles * p.tile) * FE);
     p.qs_k = r256((long long)T * FE);
     size_t o = a256(p.fused);  // the fused kernels' region first
     auto take = [&](size_t bytes) {
@@ -195,19 +201,23 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
             moe_packed_tiles(d->w_gate, type, E, rb_in, &vg, &sgp) &&
             moe_packed_tiles(d->w_up, type, E, rb_in, &vu, &sup) &&
             moe_packed_tiles(d->w_down, type, FE, rb_out, &vd, &sdp)) {
-            // gate, up, SwiGLU and down's Q8_0 input in one launch (the same bits as the three launches below)
+            // gate, up, SwiGLU and down's Q8_0 input in one launch (the same bits as the three launches below); the
+            // input handed to down in entry-tile order
             CHECK(moe_launch_grouped_swiglu(type, vg, sgp, vu, sup, 32 * value_row(type, E), 32 * scale_row(type, E),
-                                            &qx, qa.q0,
-                                            qa.d0, FE, E, p.max_tiles, ntile, te, ts, tn, tok, pair, st));
+                                            &qx, qa.q0, qa.d0, FE, E, p.max_tiles, ntile, te, ts, tn, tok, pair,
+                                            2 /* down's input in entry-tile order */, st));
+            CHECK(moe_launch_grouped_mfma(type, vd, sdp, 32 * value_row(type, FE), 32 * scale_row(type, FE), &qa, down,
+                                          E, FE, p.max_tiles, ntile, te, ts, tn, nullptr, pair,
+                                          1 /* input in entry-tile order */, st));
         } else {
             CHECK(qmatvec_launch_q8_id_batch(type, d->w_gate, rb_in, &qx, g, FE, E, p.max_tiles, p.tile, ntile, te,
                                              ts, tn, tok, pair, st));
             CHECK(qmatvec_launch_q8_id_batch(type, d->w_up, rb_in, &qx, u, FE, E, p.max_tiles, p.tile, ntile, te, ts,
                                              tn, tok, pair, st));
             CHECK(gpu_swiglu(g, u, act, T * NU * FE, &qa, st));
+            CHECK(qmatvec_launch_q8_id_batch(type, d->w_down, rb_out, &qa, down, E, FE, p.max_tiles, p.tile, ntile, te,
+                                             ts, tn, pair, pair, st));
         }
-        CHECK(qmatvec_launch_q8_id_batch(type, d->w_down, rb_out, &qa, down, E, FE, p.max_tiles, p.tile, ntile, te,
-                                         ts, tn, pair, pair, st));
         if (!sh) CHECK(gpu_moe_combine(down, wts, nullptr, nullptr, out, NU, E, T, st));
     }
     if (sh && !slot) {  // the shared expert as a dense FFN on all T tokens, then the combine

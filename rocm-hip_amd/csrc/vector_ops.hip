@@ -77,28 +77,33 @@ __global__ void __launch_bounds__(256) k_swiglu(const float* g, const float* u, 
 
 // out = w0 d0 + w1 d1 + ... in slot order (each expert's output first times exp_scale[id] when set), then the
 // shared expert (times sg when set)
+// V consecutive values per thread (V = 4: 16-byte loads and stores, n % 4 == 0 and 16-byte aligned rows); every
+// value takes the same expression in the same order either way
+template <int V>
 __global__ void __launch_bounds__(256) k_combine(const float* down, const float* wts, const float* shared,
                                                  const float* sg, const int* ids, const float* exp_scale, float* out,
                                                  int nu, int n) {
+    typedef float vec __attribute__((ext_vector_type(V)));
     const int t = blockIdx.y;
-    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int i = (blockIdx.x * 256 + threadIdx.x) * V;
     if (i >= n) return;
     const float* d = down + (size_t)t * nu * n + i;
     const float* w = wts ? wts + (size_t)t * nu : nullptr;
-    float acc;
+    auto ld = [&](const float* p) { return *(const vec*)p; };
+    vec acc;
     if (!wts) {  // weight 1 per expert
-        acc = d[0];
-        for (int j = 1; j < nu; ++j) acc += d[(size_t)j * n];
+        acc = ld(d);
+        for (int j = 1; j < nu; ++j) acc += ld(d + (size_t)j * n);
     } else if (exp_scale) {
         const int* e = ids + (size_t)t * nu;
-        acc = (d[0] * exp_scale[e[0]]) * w[0];
-        for (int j = 1; j < nu; ++j) acc += (d[(size_t)j * n] * exp_scale[e[j]]) * w[j];
+        acc = (ld(d) * exp_scale[e[0]]) * w[0];
+        for (int j = 1; j < nu; ++j) acc += (ld(d + (size_t)j * n) * exp_scale[e[j]]) * w[j];
     } else {
-        acc = w[0] * d[0];
-        for (int j = 1; j < nu; ++j) acc += w[j] * d[(size_t)j * n];
+        acc = w[0] * ld(d);
+        for (int j = 1; j < nu; ++j) acc += w[j] * ld(d + (size_t)j * n);
     }
-    if (shared) acc += sg ? shared[(size_t)t * n + i] * sg[t] : shared[(size_t)t * n + i];
-    out[(size_t)t * n + i] = acc;
+    if (shared) acc += sg ? ld(shared + (size_t)t * n + i) * sg[t] : ld(shared + (size_t)t * n + i);
+    *(vec*)(out + (size_t)t * n + i) = acc;
 }
 
 // ------------------------------------------------------------------ RMSNorm producer (src/gpu_ops.hip:24-56)
@@ -312,7 +317,10 @@ extern "C" hipError_t gpu_moe_combine_scaled(const float* down, const float* wts
                                              int T, hipStream_t stream) {
     if (!moe_lib_ready()) return hipErrorNotInitialized;
     if (n_used <= 0 || n <= 0 || T <= 0 || (exp_scale && (!ids || !wts))) return hipErrorInvalidValue;
-    return launch_kernel(k_combine, dim3((n + 255) / 256, T), dim3(256), 0, stream, down, wts, shared, sg, ids,
+    if (n % 4 == 0 && aligned(down, 16) && aligned(out, 16) && (!shared || aligned(shared, 16)))
+        return launch_kernel(k_combine<4>, dim3((n / 4 + 255) / 256, T), dim3(256), 0, stream, down, wts, shared, sg,
+                             ids, exp_scale, out, n_used, n);
+    return launch_kernel(k_combine<1>, dim3((n + 255) / 256, T), dim3(256), 0, stream, down, wts, shared, sg, ids,
                          exp_scale, out, n_used, n);
 }
 
