@@ -14,6 +14,7 @@
 #include <mutex>
 
 #include "expert_units.h"
+#include "grouped.h"
 #include "host_common.h"
 #include "qmatvec.h"
 
@@ -159,47 +160,51 @@ __global__ void __launch_bounds__(256) k_pack(const uint8_t* W, long long row_by
 
 // ------------------------------------------------------------------ MFMA operand tiles (prefill kernels)
 //
-// A second copy of a Q8_0 / ROCmFP4 / FAST matrix in the order the grouped MFMA kernel's lanes read it, so that
-// each of its 64-lane 16-byte loads is one contiguous 1 KB run (8 whole cache lines) instead of 64 pieces of
-// 64 rows. Per group of 32 rows g, in chunks of 1 KB, slot l (16 bytes) of a chunk for row 32 g + l % 32 and
-// K half h = l / 32 of a block:
-//   Q8_0:    chunk b = block b; the slot holds the block's int8 values 16 h .. 16 h + 15;
-//   ROCmFP4: chunk p = blocks 2p, 2p + 1; the slot holds 8 bytes of each: the block's nibble bytes 8 h .. 8 h + 7
-//            (low nibbles: values 8 h + i of the first 16-value half, high: values 16 + 8 h + i);
-//   FAST:    chunk p = blocks 2p, 2p + 1; 8 bytes of each: byte i = value 16 h + i | value 16 h + 8 + i << 4.
-// Scale tiles, per group g and 8-block group q: 32 row slots of 16 bytes (8 blocks' FP16 d, or UE4M3 e0 e1
-// pairs) or, for FAST, of 8 bytes (one e per block). A group's value tiles take 32 value-plane rows of bytes and
-// its scale tiles 32 scale-plane rows, so the tile copy is the size of the split-plane copy.
-__device__ __forceinline__ uint8_t fast_nibble(const uint8_t* qs, int v) {  // FAST value v (0..31) of a block
-    return v < 16 ? (qs[v] & 0x0f) : (qs[v - 16] >> 4);
+// A second copy of a Q8_0 / ROCmFP4 / FAST matrix in the order the grouped MFMA kernels' lanes read it, so that
+// each 64-lane load of it is one contiguous run instead of 64 pieces of 64 rows. Per group of 32 rows g and block
+// b, one run of 64 lane slots, slot l for row 32 g + l % 32 and K half h = l / 32:
+//   Q8_0:      16-byte slots: the block's int8 values 16 h .. 16 h + 15 (the int8 MFMA's A);
+//   FP4 types: 12-byte slots: the block's values 8 h .. 8 h + 7, then 16 + 8 h .. + 7 (the f16 MFMAs' A of each
+//              16-value half), each as the FP6 E2M3 code of codebook value / 2, 6 bits per value from bit 0 up.
+// Scale tiles, per group g and 8-block group q, 32 row slots: Q8_0 16 bytes (8 blocks' FP16 d); FP4 types 32 bytes
+// (per block the FP16 pair (e0, e1) of its UE4M3 half-scales, FAST (e, e)).
+__device__ __forceinline__ uint32_t fp4_code(const uint8_t* qs, int v) {  // code of value v (0..31) of a block
+    return v < 16 ? (qs[v] & 0x0fu) : (qs[v - 16] >> 4);
+}
+// The E2M3 code of codebook value / 2 for a 4-bit code (sign bit 3): magnitudes {0, 1, 2, 3, 4, 6, 8, 10} / 2 are
+// E2M3 0, 0.5 (subnormal 4/8), 1, 1.5, 2, 3, 4, 5 (1.25 x 4)
+__device__ __forceinline__ uint32_t fp4_to_e2m3(uint32_t c) {
+    const uint8_t tab[8] = {0x00, 0x04, 0x08, 0x0c, 0x10, 0x14, 0x18, 0x1a};
+    return tab[c & 7] | ((c & 8) << 2);  // E2M3 sign is bit 5
 }
 
 template <int TYPE>
 __global__ void __launch_bounds__(256) k_pack_tiles(const uint8_t* W, long long row_bytes, long long rows, int K,
                                                     uint8_t* V, uint8_t* S) {
     constexpr int BB = Fmt<TYPE>::BLOCK_BYTES;
-    const int nb = K / 32, nch = TYPE == QT_Q8_0 ? nb : nb / 2;
+    constexpr int SS = TYPE == QT_Q8_0 ? 16 : 12;  // value slot bytes
+    const int nb = K / 32;
     const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
-    const long long nslots = rows / 32 * nch * 64;
-    if (i < nslots) {  // value slot (g, chunk c, lane l)
+    const long long nslots = rows / 32 * nb * 64;
+    if (i < nslots) {  // value slot (g, block b, lane l)
         const int l = (int)(i & 63), h = l >> 5;
-        const long long gc = i >> 6, g = gc / nch;
-        const int c = (int)(gc - g * nch);
-        const uint8_t* row = W + (32 * g + (l & 31)) * row_bytes;
-        uint8_t out[16];
+        const long long gb = i >> 6, g = gb / nb;
+        const int b = (int)(gb - g * nb);
+        const uint8_t* blk = W + (32 * g + (l & 31)) * row_bytes + (long long)b * BB;
+        uint8_t* dst = V + SS * i;
         if constexpr (TYPE == QT_Q8_0) {
-            for (int j = 0; j < 16; ++j) out[j] = row[(long long)c * BB + 2 + 16 * h + j];
+            for (int j = 0; j < 16; ++j) dst[j] = blk[2 + 16 * h + j];
         } else {
-            for (int k = 0; k < 2; ++k) {
-                const uint8_t* qs = row + (long long)(2 * c + k) * BB;
-                for (int j = 0; j < 8; ++j)
-                    out[8 * k + j] = TYPE == QT_ROCMFP4 ? qs[8 * h + j]
-                                                        : (uint8_t)(fast_nibble(qs, 16 * h + j) |
-                                                                    fast_nibble(qs, 16 * h + 8 + j) << 4);
+            uint32_t w[3] = {0u, 0u, 0u};
+            for (int n = 0; n < 16; ++n) {
+                const int v = (n < 8 ? 8 * h : 16 + 8 * h) + (n & 7);
+                const uint32_t f = fp4_to_e2m3(fp4_code(blk, v));
+                const int bit = 6 * n;
+                w[bit >> 5] |= f << (bit & 31);
+                if ((bit & 31) > 26) w[(bit >> 5) + 1] |= f >> (32 - (bit & 31));
             }
+            for (int j = 0; j < 12; ++j) dst[j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
         }
-        uint8_t* dst = V + 16 * i;
-        for (int j = 0; j < 16; ++j) dst[j] = out[j];
         return;
     }
     const long long k = i - nslots;  // scale slot (row r, 8-block group q)
@@ -208,18 +213,17 @@ __global__ void __launch_bounds__(256) k_pack_tiles(const uint8_t* W, long long 
     const long long r = k / nq;
     const int q = (int)(k - r * nq);
     const uint8_t* row = W + r * row_bytes;
-    constexpr int SB = TYPE == QT_ROCMFP4_FAST ? 8 : 16;  // slot bytes
+    constexpr int SB = TYPE == QT_Q8_0 ? 16 : 32;  // slot bytes
     uint8_t* dst = S + ((r / 32) * nq + q) * (32 * SB) + (r & 31) * SB;
     for (int b = 0; b < 8; ++b) {
         const uint8_t* blk = row + (long long)(8 * q + b) * BB;
         if constexpr (TYPE == QT_Q8_0) {
             dst[2 * b] = blk[0];
             dst[2 * b + 1] = blk[1];
-        } else if constexpr (TYPE == QT_ROCMFP4) {
-            dst[2 * b] = blk[16];
-            dst[2 * b + 1] = blk[17];
         } else {
-            dst[b] = blk[16];
+            const uint16_t e0 = __half_as_ushort(__float2half(ue4m3_half(blk[16])));
+            const uint16_t e1 = TYPE == QT_ROCMFP4 ? __half_as_ushort(__float2half(ue4m3_half(blk[17]))) : e0;
+            *(uint32_t*)(dst + 4 * b) = (uint32_t)e0 | (uint32_t)e1 << 16;
         }
     }
 }
@@ -271,8 +275,9 @@ bool find_packed(const void* W, int type, int K, size_t row_bytes, const uint8_t
 }
 
 // The MFMA operand tiles of the registered matrix whose native rows start at W (at a 32-row group boundary): the
-// value tiles and scale tiles of W's first row group, or false
-bool find_tiles(const void* W, int type, int K, size_t row_bytes, const uint8_t** vt, const uint8_t** st) {
+// value tiles and scale tiles of W's first row group and their bytes per 32-row group, or false
+bool find_tiles(const void* W, int type, int K, size_t row_bytes, const uint8_t** vt, const uint8_t** st,
+                long long* vgs, long long* sgs) {
     if (!W) return false;
     std::lock_guard<std::mutex> lk(g_pack_mu);
     auto it = g_packed.upper_bound((uintptr_t)W);
@@ -284,8 +289,10 @@ bool find_tiles(const void* W, int type, int K, size_t row_bytes, const uint8_t*
         off % (32 * row_bytes))
         return false;
     const long long g = (long long)(off / (32 * row_bytes));
-    *vt = p.tiles + g * 32 * fmt_value_row(type, K);
-    *st = p.tiles + (size_t)p.rows * fmt_value_row(type, K) + g * 32 * fmt_scale_row(type, K);
+    *vt = p.tiles + g * 32 * tile_value_row(type, K);
+    *st = p.tiles + (size_t)p.rows * tile_value_row(type, K) + g * 32 * tile_scale_row(type, K);
+    *vgs = 32ll * tile_value_row(type, K);
+    *sgs = 32ll * tile_scale_row(type, K);
     return true;
 }
 
@@ -412,7 +419,7 @@ extern "C" size_t qmatvec_packed_bytes(int type, long long rows, int K) {
     return rows > 0 ? rb * (size_t)rows : 0;
 }
 
-// Bytes of the split-plane copy (value plane + scale plane); the tile copy, when made, is the same size
+// Bytes of the split-plane copy (value plane + scale plane)
 static size_t packed_planes_bytes(int type, long long rows, int K) {
     return (size_t)rows * (size_t)(fmt_value_row(type, K) + fmt_scale_row(type, K));
 }
@@ -428,10 +435,10 @@ static hipError_t launch_pack(const void* W, size_t rb, long long rows, int K, u
                                  (const uint8_t*)W, (long long)rb, rows, K, V, S);
     if constexpr (TYPE != QT_Q4_K) {
         if (e == hipSuccess && tiles) {
-            const long long nt = rows / 32 * (TYPE == QT_Q8_0 ? K / 32 : K / 64) * 64 + rows * (K / 256);
+            const long long nt = rows / 32 * (K / 32) * 64 + rows * (K / 256);
             e = launch_kernel(k_pack_tiles<TYPE>, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st,
                               (const uint8_t*)W, (long long)rb, rows, K, tiles,
-                              tiles + (size_t)rows * fmt_value_row(TYPE, K));
+                              tiles + (size_t)rows * tile_value_row(TYPE, K));  // scale tiles after the values
         }
     }
     return e;
@@ -451,8 +458,9 @@ extern "C" hipError_t qmatvec_pack_weights(int type, const void* W, size_t row_b
     }
     const size_t planes = packed_planes_bytes(type, rows, K);
     const bool tiled = tiles_ok(type, rows, K);
+    const size_t tile_bytes = tiled ? (size_t)rows * (size_t)(tile_value_row(type, K) + tile_scale_row(type, K)) : 0;
     void* mem = nullptr;
-    hipError_t e = hipMalloc(&mem, tiled ? 2 * planes : planes);
+    hipError_t e = hipMalloc(&mem, planes + tile_bytes);
     if (e != hipSuccess) return e;
     uint8_t* m8 = (uint8_t*)mem;
     uint8_t* tiles = tiled ? m8 + planes : nullptr;
@@ -497,8 +505,9 @@ bool moe_packed_planes(const void* W, int type, int K, size_t row_bytes, const u
 }
 
 // The MFMA operand tiles of the registered matrix at W (for the layer's grouped launches)
-bool moe_packed_tiles(const void* W, int type, int K, size_t row_bytes, const uint8_t** vt, const uint8_t** st) {
-    return find_tiles(W, type, K, row_bytes, vt, st);
+bool moe_packed_tiles(const void* W, int type, int K, size_t row_bytes, const uint8_t** vt, const uint8_t** st,
+                      long long* vgs, long long* sgs) {
+    return find_tiles(W, type, K, row_bytes, vt, st, vgs, sgs);
 }
 
 // Drop every registration (library teardown)
@@ -597,11 +606,6 @@ extern "C" hipError_t qmatvec_launch_q8(int type, const void* W, size_t row_byte
     return dense(type, W, N, y, nullptr, 0, nullptr, row_bytes, q, K, 1, N, stream);
 }
 
-bool moe_grouped_mfma_ok(int type, int N, int K);
-hipError_t moe_launch_dense_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
-                                 const qmatvec_q8* q, float* y, long long ldy, int N, int K, int T,
-                                 hipStream_t stream);
-
 // From T = 8 tokens a registered matrix runs on the MFMA kernel (its weights read once for 64 tokens), below it
 // on the matvec kernel (weights once per token, from L2 after the first)
 #define DENSE_MFMA_MIN_T 8
@@ -609,20 +613,15 @@ hipError_t moe_launch_dense_mfma(int type, const uint8_t* v, const uint8_t* s, l
 extern "C" hipError_t qmatvec_launch_q8_batch(int type, const void* W, size_t row_bytes, const qmatvec_q8* q, float* y,
                                               long long ldy, int N, int K, int T, hipStream_t stream) {
     const uint8_t *v = nullptr, *s = nullptr;
+    long long vgs = 0, sgs = 0;
     if (T >= DENSE_MFMA_MIN_T && N > 0 && ldy >= N && y && check_common(type, W, row_bytes, q, K, T) == hipSuccess &&
-        moe_grouped_mfma_ok(type, N, K) && find_tiles(W, type, K, row_bytes, &v, &s))
-        return moe_launch_dense_mfma(type, v, s, 32 * fmt_value_row(type, K), 32 * fmt_scale_row(type, K), q, y, ldy,
-                                     N, K, T, stream);
+        moe_grouped_mfma_ok(type, N, K) && find_tiles(W, type, K, row_bytes, &v, &s, &vgs, &sgs))
+        return moe_launch_dense_mfma(type, v, s, vgs, sgs, q, y, ldy, N, K, T, stream);
     return dense(type, W, N, y, nullptr, 0, nullptr, row_bytes, q, K, T, ldy, stream);
 }
 
 // Entry tiles of the grouped kernels (the MFMA kernel's 64; the per-entry fallback takes any)
 #define ENTRY_TILE 64
-
-hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
-                                   const qmatvec_q8* q, float* y, int N, int K, int max_tiles, const int32_t* n_tiles,
-                                   const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
-                                   const int32_t* in_rows, const int32_t* out_rows, int xt, hipStream_t stream);
 
 hipError_t moe_launch_entries(int type, const void* W, size_t row_bytes, const qmatvec_q8* q, float* y, int N, int K,
                               int max_tiles, const int32_t* n_tiles, const int32_t* tile_e, const int32_t* tile_start,
@@ -652,7 +651,6 @@ hipError_t moe_launch_entries(int type, const void* W, size_t row_bytes, const q
     return hipErrorInvalidDeviceFunction;
 }
 
-int moe_grouped_mfma_tile(void);
 
 // The MFMA kernel's tile where it can take the matrix (once registered), else the per-entry kernel's (any tile;
 // 64 keeps its grids filled)
@@ -675,9 +673,11 @@ extern "C" hipError_t qmatvec_launch_q8_id_batch(int type, const void* W, size_t
     if (!qmatvec_q8_supported(type, K)) return hipErrorInvalidDeviceFunction;
     if (!W || !q || row_bytes != native_row(type, K) || !aligned(W, 4)) return hipErrorInvalidValue;
     const uint8_t *v = nullptr, *s = nullptr;
-    if (moe_grouped_mfma_ok(type, N, K) && find_tiles(W, type, K, row_bytes, &v, &s))
-        return moe_launch_grouped_mfma(type, v, s, 32 * fmt_value_row(type, K), 32 * fmt_scale_row(type, K), q, y, N, K,
-                                       max_tiles, n_tiles, tile_e, tile_start, tile_n, in_rows, out_rows, 0, stream);
+    long long vgs = 0, sgs = 0;
+    if (moe_grouped_mfma_ok(type, N, K) && find_tiles(W, type, K, row_bytes, &v, &s, &vgs, &sgs))
+        return moe_launch_grouped_mfma(type, v, s, vgs, sgs, q, y, N, K,
+                                       max_tiles, n_tiles, tile_e, tile_start, tile_n, in_rows, out_rows, 0, nullptr,
+                                       stream);
     return moe_launch_entries(type, W, row_bytes, q, y, N, K, max_tiles, n_tiles, tile_e, tile_start, tile_n, in_rows,
                               out_rows, stream);
 }

@@ -1,26 +1,39 @@
-// grouped_gemm.hip -- prefill grouped expert GEMM on int8 MFMA (gfx950), over gpu_moe_group's expert tiles.
+// grouped_gemm.hip -- prefill grouped expert GEMM on MFMA (gfx950), over gpu_moe_group's expert tiles.
 //
 // Tile k (expert e, up to GG_TILE entries) times a 128-row block of e's weights: four waves, each 32 weight rows x
-// GG_TILE entries (GG_TILE / 32 MFMA tiles of 32 x 32). Per 32-value block b (one Q8_0 / FAST block, or each
-// 16-value half of a ROCmFP4 block):
-//   I = A . B on v_mfma_i32_32x32x32_i8 (32x32x16 for a ROCmFP4 half): the exact integer block dots of every
-//       (row, entry) pair; A = the weights' int8 codes (Q8_0 values, or FP4 codes decoded in registers), B =
-//       the entries' Q8_0 activation values (lane l holds row / entry l % 32 and K half l / 32, which is exactly
-//       one 16-byte half of a Q8_0 block);
-//   S = the outer product of the weight scales (d, or e0 / e1) and the entries' activation scales, on
-//       v_mfma_f32_32x32x8f16 (both scales are FP16 values, so every product is exact in fp32);
-//   acc += (float)I * S: two VALU operations per output and block.
-// Weights are read from the split-plane copy (qmatvec_pack_weights); the output rows are written to
-// y[out_rows[entry]][row]. Semantics per output: the reference's int8 expert kernels (src/matvec_q.hip:
-// 2749-2901, the integer block dot times the block's two scales, summed over blocks) in another fp32 order.
+// GG_TILE entries (GG_TILE / 32 MFMA tiles of 32 x 32). Semantics per output: the reference's int8 expert kernels
+// (src/matvec_q.hip:2749-2901: per 32-value block, the integer block dot times the block's scales, summed over
+// blocks), in another fp32 order. Two kernels by weight type:
 //
-// Measured at config 2 (2,427 tokens, gate: 221 us with 4-block stages, 205 us with 8): each workgroup waits
-// ~3x longer for its stage's operands than it computes. Not the fix, each measured: dropping the fp32 epilogue
-// (-6%), dropping the scale MFMA (0%), double-buffered stages (0%), an XCD-aware tile order (HBM fetch -40%,
-// time +5%), 128-entry tiles (weight traffic halved, +4%), register-direct operands without LDS (+50%).
-// 8-block stages read whole 128-byte lines per row and K half.
+// Q8_0 weights, on v_mfma_i32_32x32x32_i8. Per block b:
+//   I = A . B: the exact integer block dots of every (row, entry) pair; A = the weights' int8 values, B = the
+//       entries' Q8_0 activation values (lane l holds row / entry l % 32 and K half l / 32);
+//   S = the outer product of the weight and activation scales, on v_mfma_f32_32x32x8f16 (both are FP16 values,
+//       so every product is exact in fp32);
+//   acc += (float)I * S: two VALU operations per output and block.
+//
+// ROCmFP4 / FAST weights, on v_mfma_f32_32x32x16_f16 with exact operands. Every codebook value {0, 1, 2, 3, 4, 6,
+// 8, 10} (signed) times its UE4M3 (half-)block scale is exact in FP16 (at most 7 significant bits; the operand
+// tiles hold the codes as FP6 E2M3 of value / 2, which v_cvt_scalef32_pk32_f16_fp6 decodes 32 at a time with the
+// factor 2, and v_pk_mul_f16 applies the scale), and so is every Q8_0 activation value (an integer of at most 127).
+// Each product is exact in the fp32 accumulator and each 16-value half's sum of products, a multiple of its scale
+// with at most 19 significant bits, is too; the block's two halves are summed by the second MFMA. So per block:
+//   P = (e0 . codes0) . q0 + (e1 . codes1) . q1 on two f16 MFMAs, B = the activations converted to FP16 while
+//       being staged into LDS (once per workgroup, shared by its four waves);
+//   acc += P * dx, dx the entry's activation scale (the lane's own column): one VALU operation per output and
+//       block, against four for the int8 form of the same two-scale block (I and S per half).
+//
+// Weights are read from the MFMA operand tiles of qmatvec_pack_weights (one contiguous 1 KB run per 64-lane
+// load); output rows go to y[out_rows[entry]][row]; the SwiGLU variant (two matrices) writes down's Q8_0 input.
+//
+// Measured at config 2 (Q8_0, 2,427 tokens) before the operand tiles: each workgroup waited ~3x longer for its
+// stage's operands than it computed, because each 64-lane load touched 64 rows' cache lines for 16 bytes each.
+// Not the fix, each measured then: dropping the fp32 epilogue (-6%), dropping the scale MFMA (0%), double-buffered
+// stages (0%), an XCD-aware tile order (HBM fetch -40%, time +5%), 128-entry tiles (+4%), register-direct
+// operands (+50%). With the tiles the int8 kernel is VALU-bound: the conversion and FMA of every output and block.
 
 #include "expert_units.h"
+#include "grouped.h"
 #include "host_common.h"
 #include "qmatvec.h"
 
@@ -28,6 +41,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 struct GArgs {
     const uint8_t* v;  // value tiles of the stacked experts' first 32-row group (MFMA operand tiles)
@@ -51,6 +66,14 @@ struct GArgs {
     float* ad;
     int xt;               // GX_IN: the input activations are in entry-tile order (below) instead of rows;
                           // GX_OUT: the SwiGLU kernel writes down's input in entry-tile order
+    // A shared expert as more tiles of the same launch (vs null: none): tiles kr.. hold its sT entries (tokens
+    // 0..sT-1, activation rows as they are, output rows sout + token) against the tiles at vs / ss (vs2 / ss2)
+    const uint8_t* vs;
+    const uint8_t* ss;
+    const uint8_t* vs2;
+    const uint8_t* ss2;
+    int kr, sT;
+    long long sout;
 };
 #define GX_IN 1
 #define GX_OUT 2
@@ -85,33 +108,19 @@ __device__ __forceinline__ void acc_block(v16f& acc, const v16i& I, const v16f& 
     for (int j = 0; j < 16; ++j) acc[j] = fmaf((float)I[j], S[j], acc[j]);
 }
 
-// ---- Pipeline. K runs in stages of GG_KB blocks through one LDS buffer per workgroup. All operand bytes move
-// from memory to LDS with global_load_lds_dwordx4 (no register staging): lane l of such a load writes its 16
-// bytes to slot l of a 1 KB LDS run, so each load is laid out to be read back as an MFMA operand with one ds_read
-// per lane:
-//   weights: per wave and block, lane l loads row (l % 32) of the wave's 32 rows, K half l / 32 (Q8_0), or the
-//            block's 16 nibble bytes of that row (FP4 types: the lane decodes its K half from them);
-//   activations: per block and 32-entry tile, lane l loads entry (l % 32), K half l / 32;
-//   activation scales: 16-byte loads of 4 blocks per entry.
-// The weight rows' scale bytes come through registers.
+// ---- Pipeline. K runs in stages of KB blocks through one LDS buffer per workgroup. Weight tiles, activation
+// scales and (Q8_0 kernel) activations move from memory to LDS with global_load_lds_dwordx4: lane l of such a load
+// writes its 16 bytes to slot l of a 1 KB LDS run, so each run is read back as an MFMA operand with one ds_read per
+// lane. The FP4 kernel stages its activations through registers instead (converted to FP16 on the way). The weight
+// rows' scales come through registers.
 typedef __attribute__((address_space(3))) void lds_void;
-
-// Weight chunks of 1 KB per stage of KB blocks: one per block (Q8_0), one per block pair (FP4 types)
-template <int TYPE, int KB>
-struct GChunks {
-    static constexpr int PER = TYPE == QT_Q8_0 ? 1 : 2;
-    static constexpr int N = KB / PER;
-};
-
-template <int TYPE, int NM, int KB>
-struct GBuf {  // one stage of operands of NM weight matrices sharing the activations
-    uint8_t a[NM][4][GChunks<TYPE, KB>::N][1024];  // [matrix][wave][chunk][lane * 16]
-    uint8_t b[KB][GG_NT][1024];     // [block][entry tile][lane * 16]
-    float dx[KB / 4][GG_TILE][4];   // [block / 4][entry][block % 4]
-};
 
 __device__ __forceinline__ void lds_load16(const void* g, void* lds_run) {
     __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_run, 16, 0, 0);
+}
+// 12 bytes a lane: they land in 16-byte LDS slots (lane l at 16 l)
+__device__ __forceinline__ void lds_load12(const void* g, void* lds_run) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_run, 12, 0, 0);
 }
 
 template <int WAITS>
@@ -120,19 +129,46 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((WAITS & 0xf) | ((WAITS >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
-// Issue one stage's loads into B (see above); the weight scales of the stage go to wsc. Wave w loads the
-// activations of entry tile w % GG_NT, blocks w / GG_NT, + 4 / GG_NT, ... (xrow: its lane's entry row), and the
-// scales of entries GG_TILE / 4 w .. (dxr: its lane's entry row)
+// One stage of operands of NM weight matrices sharing the activations
 template <int TYPE, int NM, int KB>
-__device__ __forceinline__ void g_issue(GBuf<TYPE, NM, KB>& B, int b0, uint4 (&wsc)[NM],
+struct GBuf {  // Q8_0
+    uint8_t a[NM][4][KB][1024];   // [matrix][wave][block][lane * 16]
+    uint8_t b[KB][GG_NT][1024];   // [block][entry tile][lane * 16]
+    float dx[KB / 4][GG_TILE][4];  // [block / 4][entry][block % 4]
+};
+template <int NM, int KB>
+struct HBuf {  // FP4 types
+    uint8_t a[NM][4][KB][1024];      // [matrix][wave][block][lane * 16]: 12-byte FP6 slots
+    uint8_t b[KB][GG_NT][2][1024];   // [block][entry tile][16-value half][lane * 16]: FP16 activations
+    float dx[KB / 4][GG_TILE][4];
+};
+template <int TYPE, int NM, int KB>
+struct BufOf {
+    typedef GBuf<TYPE, NM, KB> type;
+};
+template <int NM, int KB>
+struct BufOf<QT_ROCMFP4, NM, KB> {
+    typedef HBuf<NM, KB> type;
+};
+template <int NM, int KB>
+struct BufOf<QT_ROCMFP4_FAST, NM, KB> {
+    typedef HBuf<NM, KB> type;
+};
+
+// ------------------------------------------------------------------ Q8_0: int8 MFMA
+
+// Issue one stage's loads. Wave w loads the activations of entry tile w % GG_NT, blocks w / GG_NT, + 4 / GG_NT, ...
+// (xrow: its lane's entry run), and the scales of entries GG_TILE / 4 w .. (dxr: its lane's entry row). The weight
+// scales of the stage (8 blocks' FP16 d per 16-byte slot) go to wsc.
+template <int NM, int KB>
+__device__ __forceinline__ void q_issue(GBuf<QT_Q8_0, NM, KB>& B, int b0, uint4 (&wsc)[NM],
                                         const uint8_t* const (&vt)[NM], const uint8_t* const (&st)[NM],
                                         const int8_t* xrow, int xs, const float* dxr, int w, int l) {
     constexpr int ES = GG_TILE / 4;  // entries whose scales one wave loads
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int c = 0; c < GChunks<TYPE, KB>::N; ++c)  // contiguous 1 KB chunks: one per block, or block pair
-            lds_load16(vt[m] + 1024 * (b0 / GChunks<TYPE, KB>::PER + c), B.a[m][w][c]);
+        for (int c = 0; c < KB; ++c) lds_load16(vt[m] + 1024 * (b0 + c), B.a[m][w][c]);
 #pragma unroll
     for (int j = 0; j < KB * GG_NT / 4; ++j) {
         const int bb = w / GG_NT + (4 / GG_NT) * j;
@@ -142,29 +178,20 @@ __device__ __forceinline__ void g_issue(GBuf<TYPE, NM, KB>& B, int b0, uint4 (&w
     for (int q = 0; q < KB / 4; ++q)
         if (l < ES) lds_load16(dxr + b0 + 4 * q, &B.dx[q][ES * w][0]);  // (lanes ES.. idle)
 #pragma unroll
-    for (int m = 0; m < NM; ++m) {  // the lane's row's slot of the stage's 8-block scale group
-        if constexpr (TYPE == QT_ROCMFP4_FAST) {  // 1 scale byte per block, 8-byte slots
-            const uint8_t* g = st[m] + 256 * (b0 >> 3);
-            if constexpr (KB == 4)
-                wsc[m] = make_uint4(*(const uint32_t*)(g + 4 * ((b0 >> 2) & 1)), 0u, 0u, 0u);
-            else
-                wsc[m] = make_uint4(((const uint2*)g)->x, ((const uint2*)g)->y, 0u, 0u);
-        } else {  // 2 scale bytes per block, 16-byte slots
-            const uint8_t* g = st[m] + 512 * (b0 >> 3);
-            if constexpr (KB == 4) {
-                const uint2 v = *(const uint2*)(g + 8 * ((b0 >> 2) & 1));
-                wsc[m] = make_uint4(v.x, v.y, 0u, 0u);
-            } else {
-                wsc[m] = *(const uint4*)g;
-            }
+    for (int m = 0; m < NM; ++m) {
+        const uint8_t* g = st[m] + 512 * (b0 >> 3);
+        if constexpr (KB == 4) {
+            const uint2 v = *(const uint2*)(g + 8 * ((b0 >> 2) & 1));
+            wsc[m] = make_uint4(v.x, v.y, 0u, 0u);
+        } else {
+            wsc[m] = *(const uint4*)g;
         }
     }
 }
 
-// The MFMAs of one stage from B
-template <int TYPE, int NM, int KB>
-__device__ __forceinline__ void g_compute(const GBuf<TYPE, NM, KB>& B, const uint4 (&wsc)[NM], v16f (&acc)[NM][GG_NT], int w,
-                                          int l, int lr, int kh) {
+template <int NM, int KB>
+__device__ __forceinline__ void q_compute(const GBuf<QT_Q8_0, NM, KB>& B, const uint4 (&wsc)[NM],
+                                          v16f (&acc)[NM][GG_NT], int w, int l, int lr, int kh) {
     const v16i zi = {};
 #pragma unroll
     for (int bb = 0; bb < KB; ++bb) {
@@ -173,46 +200,115 @@ __device__ __forceinline__ void g_compute(const GBuf<TYPE, NM, KB>& B, const uin
         for (int t = 0; t < GG_NT; ++t) dx[t] = B.dx[bb >> 2][32 * t + lr][bb & 3];
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
-            const uint32_t w2 = bb < 2 ? wsc[m].x : bb < 4 ? wsc[m].y : bb < 6 ? wsc[m].z : wsc[m].w;  // 2-byte
-            const uint32_t w1 = bb < 4 ? wsc[m].x : wsc[m].y;                                        // 1-byte
-            // the lane's slot: 16 bytes of block bb (Q8_0), or 8 bytes of block bb in its pair's slot (FP4 types)
-            const uint8_t* arun = TYPE == QT_Q8_0 ? B.a[m][w][bb] + 16 * l : B.a[m][w][bb >> 1] + 16 * l + 8 * (bb & 1);
-            if constexpr (TYPE == QT_ROCMFP4) {
-                const uint2 q = *(const uint2*)arun;  // nibble bytes 8 kh .. 8 kh + 7 of the row's block
-                const uint32_t ew = w2 >> (16 * (bb & 1));
+            const uint32_t w2 = bb < 2 ? wsc[m].x : bb < 4 ? wsc[m].y : bb < 6 ? wsc[m].z : wsc[m].w;
+            const uint4 q = *(const uint4*)(B.a[m][w][bb] + 16 * l);
+            const v4i A = (v4i){(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+            const float dw = h2f((uint16_t)(w2 >> (16 * (bb & 1))));
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const uint32_t sh = 4 * h;
-                    const long A =
-                        (long)(((unsigned long)fp4x4_to_i8x4(q.y >> sh) << 32) | fp4x4_to_i8x4(q.x >> sh));
-                    const float ee = ue4m3_half((ew >> (8 * h)) & 0xffu);
-                    // B, K half kh of 16-value half h: bytes 16 h + 8 kh of the block = 8 bytes of the slot of the
-                    // lane that loaded (entry, K half h)
+            for (int t = 0; t < GG_NT; ++t) {
+                const v4i Bt = *(const v4i*)(B.b[bb][t] + 16 * l);
+                acc_block(acc[m][t], __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bt, zi, 0, 0, 0),
+                          scale_outer(dw, dx[t], kh));
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// ------------------------------------------------------------------ FP4 types: exact f16 MFMA
+
+// Eight Q8_0 values (int8, two dwords) as FP16: (x ^ 0x80) in the low byte of FP16 1024 is 1024 + 128 + x, exact
+__device__ __forceinline__ uint4 i8x8_to_f16(uint32_t lo, uint32_t hi) {
+    const uint32_t tl = lo ^ 0x80808080u, th = hi ^ 0x80808080u;
+    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    auto cv = [&](uint32_t t, uint32_t sel) {
+        return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, t, sel)) - bias);
+    };
+    return make_uint4(cv(tl, 0x04010400u), cv(tl, 0x04030402u), cv(th, 0x04010400u), cv(th, 0x04030402u));
+}
+
+typedef unsigned v6u __attribute__((ext_vector_type(6)));
+typedef _Float16 v32h __attribute__((ext_vector_type(32)));
+
+// Eight decoded values (halves 8 q .. 8 q + 7 of d) times the FP16 scale pair sc: one MFMA operand
+__device__ __forceinline__ v8h scaled8(const v32h& d, int q, uint32_t sc) {
+    const h2 s = __builtin_bit_cast(h2, sc);
+    v8h r;
 #pragma unroll
-                    for (int t = 0; t < GG_NT; ++t) {
-                        const long Bt = *(const long*)(B.b[bb][t] + 16 * (lr + 32 * h) + 8 * kh);
-                        acc_block(acc[m][t], __builtin_amdgcn_mfma_i32_32x32x16_i8(A, Bt, zi, 0, 0, 0),
-                                  scale_outer(ee, dx[t], kh));
-                    }
-                }
-            } else {
-                v4i A;
-                float dw;
-                if constexpr (TYPE == QT_Q8_0) {
-                    const uint4 q = *(const uint4*)arun;
-                    A = (v4i){(int)q.x, (int)q.y, (int)q.z, (int)q.w};
-                    dw = h2f((uint16_t)(w2 >> (16 * (bb & 1))));
-                } else {  // FAST: K half kh's 16 values, value i and i + 8 in byte i's low and high nibble
-                    const uint2 q = *(const uint2*)arun;
-                    A = (v4i){(int)fp4x4_to_i8x4(q.x), (int)fp4x4_to_i8x4(q.y), (int)fp4x4_to_i8x4(q.x >> 4),
-                              (int)fp4x4_to_i8x4(q.y >> 4)};
-                    dw = ue4m3_half((w1 >> (8 * (bb & 3))) & 0xffu);
-                }
+    for (int i = 0; i < 4; ++i) {
+        const h2 p = (h2){d[8 * q + 2 * i], d[8 * q + 2 * i + 1]} * s;
+        r[2 * i] = p.x;
+        r[2 * i + 1] = p.y;
+    }
+    return r;
+}
+
+// Issue one stage: weight tiles and activation scales to LDS, this thread's activation units to registers. Unit
+// (entry tid % 64, half (tid / 64) % 2, block tid / 128 + 2 j): the 16 int8 values 16 h .. of the entry's block.
+template <int NM, int KB>
+__device__ __forceinline__ void h_issue(HBuf<NM, KB>& B, int b0, uint4 (&wsc)[NM][KB / 4],
+                                        const uint8_t* const (&vt)[NM], const uint8_t* const (&st)[NM],
+                                        const int8_t* xu, int xs, uint4 (&xb)[KB / 2], const float* dxr, int w,
+                                        int l, int tid) {
+    constexpr int ES = GG_TILE / 4;
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int c = 0; c < KB; ++c)  // 768-byte runs, 12 bytes a lane, landing in 16-byte LDS slots
+            lds_load12(vt[m] + 768 * (b0 + c), B.a[m][w][c]);
+#pragma unroll
+    for (int q = 0; q < KB / 4; ++q)
+        if (l < ES) lds_load16(dxr + b0 + 4 * q, &B.dx[q][ES * w][0]);
+#pragma unroll
+    for (int j = 0; j < KB / 2; ++j) xb[j] = *(const uint4*)(xu + xs * (b0 + (tid >> 7) + 2 * j));
+#pragma unroll
+    for (int m = 0; m < NM; ++m)  // 4 blocks' (e0, e1) FP16 pairs per 16 bytes of the row's 32-byte slot
+#pragma unroll
+        for (int q = 0; q < KB / 4; ++q) wsc[m][q] = *(const uint4*)(st[m] + 1024 * (b0 >> 3) + 16 * (((b0 >> 2) + q) & 1));
+}
+
+// This thread's activation units, converted, into the FP16 operand runs: values 0..7 of a unit to the slot of
+// (entry, K half 0) of its MFMA half, values 8..15 to that of (entry, K half 1)
+template <int NM, int KB>
+__device__ __forceinline__ void h_stage_b(HBuf<NM, KB>& B, const uint4 (&xb)[KB / 2], int tid) {
+    const int e = tid & 63, h = (tid >> 6) & 1;
+#pragma unroll
+    for (int j = 0; j < KB / 2; ++j) {
+        const int bb = (tid >> 7) + 2 * j;
+        uint8_t* run = B.b[bb][e >> 5][h];
+        *(uint4*)(run + 16 * (e & 31)) = i8x8_to_f16(xb[j].x, xb[j].y);
+        *(uint4*)(run + 16 * (32 + (e & 31))) = i8x8_to_f16(xb[j].z, xb[j].w);
+    }
+}
+
+template <int NM, int KB>
+__device__ __forceinline__ void h_compute(const HBuf<NM, KB>& B, const uint4 (&wsc)[NM][KB / 4],
+                                          v16f (&acc)[NM][GG_NT], int w, int l, int lr) {
+    const v16f z = {};
+#pragma unroll
+    for (int bp = 0; bp < KB; bp += 2) {  // a block pair: 32 FP6 codes a lane, one conversion
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            const uint3 c0 = *(const uint3*)(B.a[m][w][bp] + 16 * l);
+            const uint3 c1 = *(const uint3*)(B.a[m][w][bp + 1] + 16 * l);
+            const v32h d =
+                __builtin_amdgcn_cvt_scalef32_pk32_f16_fp6((v6u){c0.x, c0.y, c0.z, c1.x, c1.y, c1.z}, 2.0f);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int bb = bp + k;
+                const uint4 ws = wsc[m][bb >> 2];
+                const uint32_t sc = (bb & 3) == 0 ? ws.x : (bb & 3) == 1 ? ws.y : (bb & 3) == 2 ? ws.z : ws.w;
+                const v8h A0 = scaled8(d, 2 * k, __builtin_amdgcn_perm(sc, sc, 0x01000100u));      // (e0, e0)
+                const v8h A1 = scaled8(d, 2 * k + 1, __builtin_amdgcn_perm(sc, sc, 0x03020302u));  // (e1, e1)
 #pragma unroll
                 for (int t = 0; t < GG_NT; ++t) {
-                    const v4i Bt = *(const v4i*)(B.b[bb][t] + 16 * l);
-                    acc_block(acc[m][t], __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bt, zi, 0, 0, 0),
-                              scale_outer(dw, dx[t], kh));
+                    const float dx = B.dx[bb >> 2][32 * t + lr][bb & 3];
+                    const v8h B0 = *(const v8h*)(B.b[bb][t][0] + 16 * l);
+                    const v8h B1 = *(const v8h*)(B.b[bb][t][1] + 16 * l);
+                    const v16f P = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        A1, B1, __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B0, z, 0, 0, 0), 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) acc[m][t][j] = fmaf(P[j], dx, acc[m][t][j]);
                 }
             }
         }
@@ -220,15 +316,24 @@ __device__ __forceinline__ void g_compute(const GBuf<TYPE, NM, KB>& B, const uin
     }
 }
 
+// ------------------------------------------------------------------ the kernel
+
 // NM = 1: y rows (fp32) of one matrix. NM = 2, SwiGLU: gate (a.v) and up (a.v2) rows of the same block, then
 // act = SiLU(g) u (the swiglu kernel's expression) and its Q8_0 blocks -- a wave's 32 rows of one entry are one
 // block: 16 values in each of lanes l and l + 32 -- into a.aq / a.ad (the quantizer's expressions).
 template <int TYPE, int NM, int KB>
 __global__ void __launch_bounds__(256) k_grouped(GArgs a) {
-    __shared__ __attribute__((aligned(1024))) GBuf<TYPE, NM, KB> buf;
+    __shared__ __attribute__((aligned(1024))) typename BufOf<TYPE, NM, KB>::type buf;
+    constexpr bool F16 = TYPE != QT_Q8_0;
     const int k = blockIdx.y;
+    const bool shk = a.vs && k >= a.kr;  // a shared-expert tile
     int e, st, cnt;
-    if (a.n_tiles) {
+    if (shk) {
+        st = (k - a.kr) * GG_TILE;
+        if (st >= a.sT) return;
+        e = 0;
+        cnt = min(GG_TILE, a.sT - st);
+    } else if (a.n_tiles) {
         if (k >= *a.n_tiles) return;
         e = a.tile_e[k];
         st = a.tile_start[k];
@@ -240,36 +345,25 @@ __global__ void __launch_bounds__(256) k_grouped(GArgs a) {
         cnt = min(GG_TILE, a.T - st);
     }
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lr = l & 31, kh = l >> 5;
-    auto in_row = [&](int i) { return a.in_rows ? a.in_rows[st + i] : st + i; };
-    auto out_row = [&](int i) { return a.out_rows ? a.out_rows[st + i] : st + i; };
+    auto in_row = [&](int i) { return !shk && a.in_rows ? a.in_rows[st + i] : st + i; };
+    auto out_row = [&](int i) { return shk ? a.sout + st + i : a.out_rows ? a.out_rows[st + i] : st + i; };
     const int K = a.K, nb = K / 32;
     // the wave's 32-row group of the stacked matrix (the launcher requires N % 128 == 0 and K % 256 == 0) and
-    // this lane's slots in its value and scale tiles
+    // this lane's slots in its value and scale tiles (scale slots: 16 bytes per 8 blocks for Q8_0, 32 for FP4)
     const int r0 = blockIdx.x * GG_ROWS + 32 * w;
     const long long grp = ((long long)e * a.N + r0) / 32;
-    constexpr int SB = TYPE == QT_ROCMFP4_FAST ? 8 : 16;
+    constexpr int SB = F16 ? 32 : 16;
+    constexpr int VS = F16 ? 12 : 16;  // value slot bytes
     const uint8_t* vt[NM];
     const uint8_t* sct[NM];
-    vt[0] = a.v + grp * a.vrb + 16 * l;
-    sct[0] = a.s + grp * a.srb + SB * lr;
+    vt[0] = (shk ? a.vs : a.v) + grp * a.vrb + VS * l;
+    sct[0] = (shk ? a.ss : a.s) + grp * a.srb + SB * lr;
     if constexpr (NM == 2) {
-        vt[1] = a.v2 + grp * a.vrb + 16 * l;
-        sct[1] = a.s2 + grp * a.srb + SB * lr;
+        vt[1] = (shk ? a.vs2 : a.v2) + grp * a.vrb + VS * l;
+        sct[1] = (shk ? a.ss2 : a.s2) + grp * a.srb + SB * lr;
     }
-    // the entry rows this lane loads: activations of entry 32 (w % GG_NT) + lr, scales of entry GG_TILE / 4 w + l
     const int de = min(GG_TILE / 4 * w + (l & (GG_TILE / 4 - 1)), cnt - 1);  // the entry whose scales this lane loads
-    const int8_t* xrow;
-    const float* dxr;
-    int xs;  // bytes from one block's operand run to the next
-    if (a.xt & GX_IN) {
-        xrow = a.xq + ((long long)k * nb * GG_NT + w % GG_NT) * 1024 + 16 * l;
-        xs = GG_NT * 1024;
-        dxr = a.xd + ((long long)k * GG_TILE + de) * nb;
-    } else {
-        xrow = a.xq + (long long)in_row(min(32 * (w % GG_NT) + lr, cnt - 1)) * K + 16 * kh;
-        xs = 32;
-        dxr = a.xd + (long long)in_row(de) * nb;
-    }
+    const float* dxr = a.xd + ((a.xt & GX_IN) ? (long long)k * GG_TILE + de : (long long)in_row(de)) * nb;
 
     v16f acc[NM][GG_NT];
 #pragma unroll
@@ -277,15 +371,47 @@ __global__ void __launch_bounds__(256) k_grouped(GArgs a) {
 #pragma unroll
         for (int t = 0; t < GG_NT; ++t) acc[m][t] = (v16f){};
     const int nst = nb / KB;
-    uint4 wsc[NM];
-    for (int s = 0; s < nst; ++s) {
-        // one stage: its loads, then (with several workgroups per CU hiding the latency of each other's loads)
-        // its MFMAs
-        g_issue<TYPE, NM, KB>(buf, s * KB, wsc, vt, sct, xrow, xs, dxr, w, l);
-        wait_vm<0>();
-        __syncthreads();
-        g_compute<TYPE, NM, KB>(buf, wsc, acc, w, l, lr, kh);
-        __syncthreads();
+    if constexpr (!F16) {
+        // this lane's activation run: entry 32 (w % GG_NT) + lr, K half kh
+        const int8_t* xrow;
+        int xs;  // bytes from one block's run to the next
+        if (a.xt & GX_IN) {
+            xrow = a.xq + ((long long)k * nb * GG_NT + w % GG_NT) * 1024 + 16 * l;
+            xs = GG_NT * 1024;
+        } else {
+            xrow = a.xq + (long long)in_row(min(32 * (w % GG_NT) + lr, cnt - 1)) * K + 16 * kh;
+            xs = 32;
+        }
+        uint4 wsc[NM];
+        for (int s = 0; s < nst; ++s) {
+            q_issue<NM, KB>(buf, s * KB, wsc, vt, sct, xrow, xs, dxr, w, l);
+            wait_vm<0>();
+            __syncthreads();
+            q_compute<NM, KB>(buf, wsc, acc, w, l, lr, kh);
+            __syncthreads();
+        }
+    } else {
+        // this thread's activation unit: entry tid % 64, 16-value half (tid / 64) % 2
+        const int ue = tid & 63, uh = (tid >> 6) & 1;
+        const int8_t* xu;
+        int xs;
+        if (a.xt & GX_IN) {
+            xu = a.xq + ((long long)k * nb * GG_NT + (ue >> 5)) * 1024 + 16 * (32 * uh + (ue & 31));
+            xs = GG_NT * 1024;
+        } else {
+            xu = a.xq + (long long)in_row(min(ue, cnt - 1)) * K + 16 * uh;
+            xs = 32;
+        }
+        uint4 wsc[NM][KB / 4];
+        uint4 xb[KB / 2];
+        for (int s = 0; s < nst; ++s) {
+            h_issue<NM, KB>(buf, s * KB, wsc, vt, sct, xu, xs, xb, dxr, w, l, tid);
+            wait_vm<0>();
+            h_stage_b<NM, KB>(buf, xb, tid);
+            __syncthreads();
+            h_compute<NM, KB>(buf, wsc, acc, w, l, lr);
+            __syncthreads();
+        }
     }
     // acc[m][t][j] is C[row 8 (j / 4) + 4 kh + j % 4][entry 32 t + lr] of the wave's 32 x GG_TILE block
     if constexpr (NM == 1) {
@@ -314,7 +440,7 @@ __global__ void __launch_bounds__(256) k_grouped(GArgs a) {
                 const bool xo = a.xt & GX_OUT;
                 const long long pr = xo ? (long long)k * GG_TILE + 32 * t + lr : out_row(32 * t + lr);
                 int8_t* q = xo ? a.aq + (((long long)k * (a.N / 32) + r0 / 32) * GG_NT + t) * 1024 + 16 * lr
-                                 : a.aq + pr * a.N + r0;
+                               : a.aq + pr * a.N + r0;
 #pragma unroll
                 for (int m4 = 0; m4 < 4; ++m4) {  // rows 8 m4 + 4 kh .. + 3: four consecutive bytes
                     uint32_t pk = 0;
@@ -339,13 +465,28 @@ bool moe_grouped_mfma_ok(int type, int N, int K) {
 // The entry tile the MFMA kernel takes
 int moe_grouped_mfma_tile(void) { return GG_TILE; }
 
+// The shared-expert tiles of a launch (GArgs::vs ..); sh null: none
+static void bind_shared(GArgs& a, const GShared* sh, int max_tiles, dim3& g) {
+    if (!sh) return;
+    a.vs = sh->v;
+    a.ss = sh->s;
+    a.vs2 = sh->v2;
+    a.ss2 = sh->s2;
+    a.kr = max_tiles;
+    a.sT = sh->T;
+    a.sout = sh->out0;
+    g.y += (sh->T + GG_TILE - 1) / GG_TILE;
+}
+
 hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
                                    const qmatvec_q8* q, float* y, int N, int K, int max_tiles, const int32_t* n_tiles,
                                    const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
-                                   const int32_t* in_rows, const int32_t* out_rows, int xt, hipStream_t stream) {
+                                   const int32_t* in_rows, const int32_t* out_rows, int xt, const GShared* sh,
+                                   hipStream_t stream) {
     GArgs a = {v,      s,       vrb,      srb, q->q0, q->d0, y,       N,       K,       n_tiles, tile_e,
                tile_start, tile_n, in_rows, out_rows, N, 0, nullptr, nullptr, nullptr, nullptr, xt};
-    const dim3 g(N / GG_ROWS, max_tiles), b(256);
+    dim3 g(N / GG_ROWS, max_tiles), b(256);
+    bind_shared(a, sh, max_tiles, g);
     switch (type) {
     case QT_Q8_0: return launch_kernel(k_grouped<QT_Q8_0, 1, GG_KB>, g, b, 0, stream, a);
     case QT_ROCMFP4: return launch_kernel(k_grouped<QT_ROCMFP4, 1, GG_KB>, g, b, 0, stream, a);
@@ -355,15 +496,18 @@ hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s,
 }
 
 // Gate and up of the same tiles in one launch, then SwiGLU and down's Q8_0 input (aq rows of N, ad per 32; in
-// entry-tile order with xt = GX_OUT) instead of the gate / up outputs. xt: GX_IN / GX_OUT flags (GArgs::xt)
+// entry-tile order with xt = GX_OUT) instead of the gate / up outputs. xt: GX_IN / GX_OUT flags (GArgs::xt); sh: a
+// shared expert's tiles after the max_tiles routed ones (its entries' rows in entry-tile order continue there)
 hipError_t moe_launch_grouped_swiglu(int type, const uint8_t* vg, const uint8_t* sg, const uint8_t* vu,
                                      const uint8_t* su, long long vrb, long long srb, const qmatvec_q8* q, int8_t* aq,
                                      float* ad, int N, int K, int max_tiles, const int32_t* n_tiles,
                                      const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
-                                     const int32_t* in_rows, const int32_t* out_rows, int xt, hipStream_t stream) {
+                                     const int32_t* in_rows, const int32_t* out_rows, int xt, const GShared* sh,
+                                     hipStream_t stream) {
     GArgs a = {vg,         sg,     vrb,     srb,      q->q0, q->d0, nullptr, N,  K,  n_tiles, tile_e,
                tile_start, tile_n, in_rows, out_rows, N,     0,     vu,      su, aq, ad, xt};
-    const dim3 g(N / GG_ROWS, max_tiles), b(256);
+    dim3 g(N / GG_ROWS, max_tiles), b(256);
+    bind_shared(a, sh, max_tiles, g);
     switch (type) {
     case QT_Q8_0: return launch_kernel(k_grouped<QT_Q8_0, 2, GG_KB2>, g, b, 0, stream, a);
     case QT_ROCMFP4: return launch_kernel(k_grouped<QT_ROCMFP4, 2, GG_KB2>, g, b, 0, stream, a);

@@ -9,6 +9,7 @@
 #include <atomic>
 
 #include "gpu_ops.h"
+#include "grouped.h"
 #include "qmatvec.h"
 
 struct FArgs;
@@ -20,17 +21,6 @@ bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits,
 bool moe_fused_multi_try(const moe_layer_desc* d, const float* x, const float* logits, int T, float* out,
                          int* ids_out, float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err);
 
-bool moe_packed_tiles(const void* W, int type, int K, size_t row_bytes, const uint8_t** vt, const uint8_t** st);
-bool moe_grouped_mfma_ok(int type, int N, int K);
-hipError_t moe_launch_grouped_swiglu(int type, const uint8_t* vg, const uint8_t* sg, const uint8_t* vu,
-                                     const uint8_t* su, long long vrb, long long srb, const qmatvec_q8* q, int8_t* aq,
-                                     float* ad, int N, int K, int max_tiles, const int32_t* n_tiles,
-                                     const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
-                                     const int32_t* in_rows, const int32_t* out_rows, int xt, hipStream_t stream);
-hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
-                                   const qmatvec_q8* q, float* y, int N, int K, int max_tiles, const int32_t* n_tiles,
-                                   const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
-                                   const int32_t* in_rows, const int32_t* out_rows, int xt, hipStream_t stream);
 
 hipError_t moe_quantize_q8_0(const float* x, int n, const qmatvec_q8* q, hipStream_t stream);
 
@@ -43,9 +33,6 @@ namespace {
 size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
 int r256(long long k) { return (int)((k + 255) / 256 * 256); }
 
-// Split-plane row bytes (values, scales) of the Q8_0-activation types (8: Q8_0, 100: ROCmFP4, 101: FAST)
-long long value_row(int type, int k) { return type == 8 ? k : k / 2; }
-long long scale_row(int type, int k) { return type == 101 ? k / 32 : k / 16; }
 
 size_t row_size(int type, int k) {
     switch (type) {
@@ -74,8 +61,10 @@ Plan plan(const moe_layer_desc* d, int T) {
     p.fused = moe_fused_scratch_bytes(d, T < FUSED_MAX_T ? T : FUSED_MAX_T);
     p.max_tiles = gpu_moe_max_tiles(T, NU, NE, p.tile);
     p.qx_k = r256((long long)T * E);
-    // down's input: pair rows, or (the fused prefill) entry tiles of p.tile rows each
-    p.qa_k = r256(std::max((long long)T * p.NS, (long long)p.max_tiles * p.tile) * FE);
+    // down's input: pair rows, or (the fused prefill) entry tiles of p.tile rows each, the shared expert's after
+    // the routed ones
+    const long long sh_tiles = sh ? (T + p.tile - 1) / p.tile : 0;
+    p.qa_k = r256(std::max((long long)T * p.NS, ((long long)p.max_tiles + sh_tiles) * p.tile) * FE);
     p.qs_k = r256((long long)T * FE);
     size_t o = a256(p.fused);  // the fused kernels' region first
     auto take = [&](size_t bytes) {
@@ -167,6 +156,7 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
         CHECK(moe_quantize_q8_0(x, T * E, &qx, st));
 
     const bool slot = T == 1 && sh;  // moe_core_one: the shared expert as slot NU
+    bool shared_done = false;  // the prefill path ran the shared expert and the combine with the routed experts
     if (T < 8) {
         const int ns = slot ? NU + 1 : NU;
         CHECK(gpu_moe_router(lg, x, d->w_shexp, ids, wts, sg, NE, NU, E, T, st, ns));
@@ -197,18 +187,33 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
         CHECK(gpu_moe_group_ws(ids, T, NU, NE, p.tile, tok, pair, ntile, te, ts, tn, s + p.gws,
                                gpu_moe_group_ws_bytes(T, NE), st));
         const uint8_t *vg = nullptr, *sgp = nullptr, *vu = nullptr, *sup = nullptr, *vd = nullptr, *sdp = nullptr;
+        long long gvs = 0, gss = 0, dvs = 0, dss = 0;  // tile bytes per 32-row group (gate and up alike, down)
         if (mode && moe_grouped_mfma_ok(type, FE, E) && moe_grouped_mfma_ok(type, E, FE) &&
-            moe_packed_tiles(d->w_gate, type, E, rb_in, &vg, &sgp) &&
-            moe_packed_tiles(d->w_up, type, E, rb_in, &vu, &sup) &&
-            moe_packed_tiles(d->w_down, type, FE, rb_out, &vd, &sdp)) {
+            moe_packed_tiles(d->w_gate, type, E, rb_in, &vg, &sgp, &gvs, &gss) &&
+            moe_packed_tiles(d->w_up, type, E, rb_in, &vu, &sup, &gvs, &gss) &&
+            moe_packed_tiles(d->w_down, type, FE, rb_out, &vd, &sdp, &dvs, &dss)) {
+            // The shared expert (when its matrices have tiles too) as more tiles of the same two launches: its
+            // outputs are rows T NU .. of down
+            GShared shg = {}, shd = {};
+            long long v0, s0;
+            const bool merged = sh && moe_packed_tiles(d->s_gate, type, E, rb_in, &shg.v, &shg.s, &v0, &s0) &&
+                                moe_packed_tiles(d->s_up, type, E, rb_in, &shg.v2, &shg.s2, &v0, &s0) &&
+                                moe_packed_tiles(d->s_down, type, FE, rb_out, &shd.v, &shd.s, &v0, &s0);
+            shg.T = shd.T = T;
+            shg.out0 = shd.out0 = (long long)T * NU;
             // gate, up, SwiGLU and down's Q8_0 input in one launch (the same bits as the three launches below); the
             // input handed to down in entry-tile order
-            CHECK(moe_launch_grouped_swiglu(type, vg, sgp, vu, sup, 32 * value_row(type, E), 32 * scale_row(type, E),
+            CHECK(moe_launch_grouped_swiglu(type, vg, sgp, vu, sup, gvs, gss,
                                             &qx, qa.q0, qa.d0, FE, E, p.max_tiles, ntile, te, ts, tn, tok, pair,
-                                            2 /* down's input in entry-tile order */, st));
-            CHECK(moe_launch_grouped_mfma(type, vd, sdp, 32 * value_row(type, FE), 32 * scale_row(type, FE), &qa, down,
+                                            2 /* down's input in entry-tile order */, merged ? &shg : nullptr, st));
+            CHECK(moe_launch_grouped_mfma(type, vd, sdp, dvs, dss, &qa, down,
                                           E, FE, p.max_tiles, ntile, te, ts, tn, nullptr, pair,
-                                          1 /* input in entry-tile order */, st));
+                                          1 /* input in entry-tile order */, merged ? &shd : nullptr, st));
+            if (merged) {
+                CHECK(gpu_moe_combine(down, wts, down + (size_t)T * NU * E, d->w_shexp ? sg : nullptr, out, NU, E, T,
+                                      st));
+                shared_done = true;
+            }
         } else {
             CHECK(qmatvec_launch_q8_id_batch(type, d->w_gate, rb_in, &qx, g, FE, E, p.max_tiles, p.tile, ntile, te,
                                              ts, tn, tok, pair, st));
@@ -220,7 +225,7 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
         }
         if (!sh) CHECK(gpu_moe_combine(down, wts, nullptr, nullptr, out, NU, E, T, st));
     }
-    if (sh && !slot) {  // the shared expert as a dense FFN on all T tokens, then the combine
+    if (sh && !slot && !shared_done) {  // the shared expert as a dense FFN on all T tokens, then the combine
         float* sgt = (float*)(s + p.sg_);
         float* sut = (float*)(s + p.su);
         float* sact = (float*)(s + p.sact);
