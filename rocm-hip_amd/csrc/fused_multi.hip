@@ -20,7 +20,6 @@
 #include "qmatvec.h"
 
 #define FM_MAX_U 65  // union slots: at most FD_MAX_T * NU (<= 64) experts and the shared one
-int moe_device_cus(void);
 
 #ifndef FM_HALVES
 #define FM_HALVES 1  // units per round of the persistent gate / up kernel (2: halves of 8 waves, 8 rows each)

@@ -8,6 +8,9 @@
 // 1 once qmatvec_init / gpu_ops_init found a gfx950 device (either one initialises the whole library)
 extern "C" int moe_lib_ready(void);
 
+// Compute units of the initialised device (persistent grids size themselves by it)
+int moe_device_cus(void);
+
 template <typename T>
 struct same_type {
     typedef T type;

@@ -61,3 +61,11 @@ def test_launch_before_init_fails_loudly():
     lib = moe_hip.load_library()
     # without a device (or before init) the library refuses to launch rather than fall back
     assert lib.qmatvec_quantize(None, 256, None, None) != 0
+
+
+def test_no_unresolved_library_symbols():
+    """Every symbol the library needs is defined in it or versioned by a system library (a missing internal
+    definition would only fail at load time on the GPU box)."""
+    out = subprocess.run(["nm", "-D", "--undefined-only", moe_hip.LIB_PATH], capture_output=True, text=True).stdout
+    missing = [line.split()[-1] for line in out.splitlines() if " U " in line and "@" not in line]
+    assert not missing, missing
