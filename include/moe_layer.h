@@ -45,6 +45,16 @@ size_t moe_layer_scratch_bytes(const moe_layer_desc* d, int max_t);
 hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x, const float* logits, int T, float* out,
                              int* ids_out, float* wts_out, void* scratch, size_t scratch_bytes, hipStream_t stream);
 
+// No counterpart in the reference as one call (its engine issues gpu_add_rmsnorm, then the layer): the RMSNorm
+// producer fused in front of the layer. y = RMSNorm(x_in + add) * w_norm (add NULL: of x_in; w_norm NULL: no gamma;
+// eps as gpu_add_rmsnorm), x_out = x_in + add (add set: x_out required), then out = MoE(y) as moe_layer_forward.
+// The same bits as gpu_add_rmsnorm followed by moe_layer_forward; at T == 1 on the fused kernels the normalization
+// happens inside their first kernel (one launch less per layer). Same scratch as moe_layer_forward.
+hipError_t moe_layer_forward_norm(const moe_layer_desc* d, const float* x_in, const float* add, float* x_out,
+                                  const float* w_norm, float eps, const float* logits, int T, float* out,
+                                  int* ids_out, float* wts_out, void* scratch, size_t scratch_bytes,
+                                  hipStream_t stream);
+
 // No counterpart in the reference. Whether T == 1 calls may use the fused kernels (1, the default) or always take
 // the per-operation launches (0); process-wide. Profiling only: 0x100 | mask launches just the fused kernels in
 // mask (bit 0: logits / quantize, bit 1: routing + gate / up, bit 2: down + combine), which then read what earlier

@@ -42,8 +42,43 @@ struct FArgs {
     float* adk;
     int32_t* absk;
     unsigned long long* stamps;  // optional timestamps (profiling, one token): [workgroup][8], nullptr: none
+    // norm set (T = 1): the layer's input is RMSNorm(x + add) * w_norm, formed by kernel 1 (gpu_add_rmsnorm's
+    // expressions); x_out (when add is set) receives x + add
+    const float* add;
+    const float* w_norm;
+    float* x_out;
+    float eps;
+    int norm;
     int T, E, NE, NU, FE, NS, has_gate;
 };
+
+// The RMSNorm producer fused into the layer (moe_layer_forward_norm): its arguments
+struct FNorm {
+    const float* add;
+    const float* w;
+    float* x_out;
+    float eps;
+};
+
+// The RMSNorm producer's first pass (src/gpu_ops.hip:24-56, gpu_add_rmsnorm): thread t's values t + 256 k (k < 16,
+// n <= 4096) of x (+ add) into keep, and the row's 1 / sqrt(mean(v^2) + eps). Every caller shares these expressions.
+__device__ __forceinline__ float rms_first_pass(const float* xr, const float* ar, int n, float eps, float (&keep)[16],
+                                                float* part) {
+    const int t = threadIdx.x;
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int i = t + 256 * k;
+        keep[k] = i < n ? (ar ? xr[i] + ar[i] : xr[i]) : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) ss += keep[k] * keep[k];
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) part[t >> 6] = ss;
+    __syncthreads();
+    const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+    return 1.0f / sqrtf(tot / (float)n + eps);
+}
 
 // Timestamp k of this workgroup (the 100 MHz wall clock), when stamps are requested: kernel 1 uses slots 0, 1,
 // kernel 2 slots 2..4 and 7, kernel 3 slots 5, 6 of row blockIdx.x of a [max grid][8] table

@@ -31,10 +31,27 @@
 // the shared gate (the last workgroup)
 __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
     __shared__ float part[4];
+    __shared__ __align__(16) float ys[FD_MAX_E];
     const int tid = threadIdx.x, E = a.E;
     stamp(a, 0);
+    const float* xv = a.x;
+    if (a.norm) {  // every workgroup forms the normalized input itself (E <= 4096 values, from L2)
+        float keep[16];
+        const float inv = rms_first_pass(a.x, a.add, E, a.eps, keep, part);
+        const bool res = blockIdx.x == 0 && a.add && a.x_out;  // workgroup 0 writes the residual
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int i = tid + 256 * k;
+            if (i < E) {
+                ys[i] = keep[k] * inv * (a.w_norm ? a.w_norm[i] : 1.0f);
+                if (res) a.x_out[i] = keep[k];
+            }
+        }
+        __syncthreads();
+        xv = ys;
+    }
     if ((int)blockIdx.x < a.NE) {
-        const float y = f32_row_dot(a.w_router + (size_t)blockIdx.x * E, a.x, E, part);
+        const float y = f32_row_dot(a.w_router + (size_t)blockIdx.x * E, xv, E, part);
         if (tid == 0) a.logits[blockIdx.x] = y;
         stamp(a, 1);
         return;
@@ -43,18 +60,18 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
         __shared__ Q8Smem sh;
         const int blk = blockIdx.x - a.NE;
         if (blk < E / 256) {
-            q8_quantize_256(a.x[blk * 256 + tid], true, blk, tid, sh, a.xo);
+            q8_quantize_256(xv[blk * 256 + tid], true, blk, tid, sh, a.xo);
             stamp(a, 1);
             return;
         }
     }
     if ((int)blockIdx.x == a.NE + (a.xo.qK ? E / 256 : 1)) {  // the shared expert's gate
-        const float g = shexp_gate(a.x, a.w_shexp, E, part);
+        const float g = shexp_gate(xv, a.w_shexp, E, part);
         if (tid == 0) a.sg[0] = g;
         stamp(a, 1);
         return;
     }
-    quantize_row_q8_0(a.x, E, a.xq, a.xd);  // x quantized for gate / up
+    quantize_row_q8_0(xv, E, a.xq, a.xd);  // x quantized for gate / up
     stamp(a, 1);
 }
 
@@ -314,11 +331,18 @@ extern "C" void moe_layer_fused_stamps(void* stamps) { g_stamps = (unsigned long
 unsigned long long* moe_fused_stamps_ptr() { return g_stamps; }
 
 bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits, float* out, int* ids_out,
-                   float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err) {
+                   float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err, const FNorm* norm) {
     FArgs a = {};
     a.stamps = g_stamps;
     if (!moe_fused_prepare(d, a)) return false;
     a.x = x;
+    if (norm) {
+        a.norm = 1;
+        a.add = norm->add;
+        a.w_norm = norm->w;
+        a.x_out = norm->x_out;
+        a.eps = norm->eps;
+    }
     a.logits_in = logits;
     a.out = out;
     a.ids_out = ids_out;

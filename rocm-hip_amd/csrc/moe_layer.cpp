@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <atomic>
 
+#include "fused_common.h"
 #include "gpu_ops.h"
 #include "grouped.h"
 #include "qmatvec.h"
@@ -17,7 +18,7 @@ size_t moe_fused_scratch_bytes(const moe_layer_desc* d, int T);
 
 // The fused decode kernel's arguments are built in fused_decode.hip; this file only sees these entry points
 bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits, float* out, int* ids_out,
-                   float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err);
+                   float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err, const FNorm* norm);
 bool moe_fused_multi_try(const moe_layer_desc* d, const float* x, const float* logits, int T, float* out,
                          int* ids_out, float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err);
 
@@ -47,7 +48,7 @@ size_t row_size(int type, int k) {
 // Scratch carve-up; every piece 256-byte aligned
 struct Plan {
     size_t fused, logits, ids, wts, sg, qx, g, u, act, qa, down, sg_, su, sact, qs, sout, tok, pair, ntile, te, ts, tn,
-        gws, total;
+        gws, ynorm, total;
     int NS, qx_k, qa_k, qs_k, max_tiles, tile;
 };
 
@@ -94,6 +95,7 @@ Plan plan(const moe_layer_desc* d, int T) {
     p.ts = take((size_t)p.max_tiles * 4);
     p.tn = take((size_t)p.max_tiles * 4);
     p.gws = take(gpu_moe_group_ws_bytes(T, NE));
+    p.ynorm = take((size_t)T * E * 4);  // moe_layer_forward_norm's normalized input (unfused paths)
     p.total = o;
     return p;
 }
@@ -127,7 +129,7 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
     if (T <= FUSED_MAX_T && mode) {
         hipError_t e = hipSuccess;
         const int kernels = mode == 1 ? 7 : mode & 7;
-        if (T == 1 ? moe_fused_try(d, x, logits_in, out, ids_out, wts_out, scratch, kernels, st, &e)
+        if (T == 1 ? moe_fused_try(d, x, logits_in, out, ids_out, wts_out, scratch, kernels, st, &e, nullptr)
                    : moe_fused_multi_try(d, x, logits_in, T, out, ids_out, wts_out, scratch, kernels, st, &e))
             return e;
     }
@@ -243,4 +245,26 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
                                hipMemcpyDeviceToDevice, st));
     if (wts_out) CHECK(hipMemcpyAsync(wts_out, wts, (size_t)T * NU * 4, hipMemcpyDeviceToDevice, st));
     return hipSuccess;
+}
+
+// The producer fused in: y = RMSNorm(x_in + add) * w_norm, x_out = x_in + add, then the layer on y. T == 1 with the
+// fused decode kernels forms y inside their first kernel; every other case runs gpu_add_rmsnorm into scratch first.
+// Either way the results equal gpu_add_rmsnorm followed by moe_layer_forward bit for bit.
+extern "C" hipError_t moe_layer_forward_norm(const moe_layer_desc* d, const float* x_in, const float* add,
+                                             float* x_out, const float* w_norm, float eps, const float* logits, int T,
+                                             float* out, int* ids_out, float* wts_out, void* scratch,
+                                             size_t scratch_bytes, hipStream_t st) {
+    if (!d || !x_in || !out || T <= 0 || !scratch || ((uintptr_t)scratch & 255) || (add && !x_out))
+        return hipErrorInvalidValue;
+    const Plan p = plan(d, T);
+    if (scratch_bytes < p.total) return hipErrorInvalidValue;
+    const int mode = g_fused.load(std::memory_order_relaxed);
+    if (T == 1 && mode == 1 && d->n_embd <= 4096) {
+        const FNorm nm = {add, w_norm, x_out, eps};
+        hipError_t e = hipSuccess;
+        if (moe_fused_try(d, x_in, logits, out, ids_out, wts_out, scratch, 7, st, &e, &nm)) return e;
+    }
+    float* y = (float*)((char*)scratch + p.ynorm);
+    CHECK(gpu_add_rmsnorm(x_in, add, x_out, w_norm, y, d->n_embd, T, eps, nullptr, st));
+    return moe_layer_forward(d, y, logits, T, out, ids_out, wts_out, scratch, scratch_bytes, st);
 }

@@ -120,26 +120,21 @@ __global__ void __launch_bounds__(256) k_add_rmsnorm(const float* x_in, const fl
     constexpr int KEEP = 16;
     float keep[KEEP];
     const bool kept = n <= 256 * KEEP;
-    float ss = 0.0f;
+    float inv;
     if (kept) {
-#pragma unroll
-        for (int k = 0; k < KEEP; ++k) {
-            const int i = t + 256 * k;
-            keep[k] = i < n ? (ar ? xr[i] + ar[i] : xr[i]) : 0.0f;
-        }
-#pragma unroll
-        for (int k = 0; k < KEEP; ++k) ss += keep[k] * keep[k];
+        inv = rms_first_pass(xr, ar, n, eps, keep, part);
     } else {
+        float ss = 0.0f;
         for (int i = t; i < n; i += 256) {
             const float v = ar ? xr[i] + ar[i] : xr[i];
             ss += v * v;
         }
+        ss = wave_sum(ss);
+        if ((t & 63) == 0) part[t >> 6] = ss;
+        __syncthreads();
+        const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+        inv = 1.0f / sqrtf(tot / (float)n + eps);
     }
-    ss = wave_sum(ss);
-    if ((t & 63) == 0) part[t >> 6] = ss;
-    __syncthreads();
-    const float tot = (part[0] + part[1]) + (part[2] + part[3]);
-    const float inv = 1.0f / sqrtf(tot / (float)n + eps);
     const int nb = (n + 255) / 256;
     auto block = [&](int b, float xv) {  // block b of 256 values: outputs, then the quantizer (uniform call)
         const int i = b * 256 + t;
