@@ -66,8 +66,8 @@ __global__ void __launch_bounds__(256) k_expert_mv(MvArgs a) {
     const int nrows = mi & 1 ? a.N2 : a.N;
     if (row0 - grp >= nrows) return;  // the whole wave is past the end (uniform per wave)
     const long long rbase = e >= 0 ? (long long)e * nrows : 0;
-    const uint8_t* vbase = a.v[mi] + rbase * a.vrb;
-    const uint8_t* sbase = PACKED ? a.s[mi] + rbase * a.srb : nullptr;
+    const uint8_t* vbase = pick(a.v, mi) + rbase * a.vrb;
+    const uint8_t* sbase = PACKED ? pick(a.s, mi) + rbase * a.srb : nullptr;
     const long long in_row = a.ids && a.x_per_slot ? (long long)t * a.n_used + slot : t;
     const int8_t* xq;
     const float* xd;

@@ -103,8 +103,8 @@ __global__ void __launch_bounds__(64 * (64 / FD_GU_RW)) k_fd_gate_up(FArgs a) {
     const int mat = w / WPM;  // the first WPM waves: gate rows; the next WPM: up rows
     const int mi = e >= 0 ? mat : 3 + mat;
     const long long rbase = e >= 0 ? (long long)e * FE : 0;
-    const uint8_t* vb = a.v[mi] + rbase * a.vrb_in;
-    const uint8_t* sb = a.s[mi] + rbase * a.srb_in;
+    const uint8_t* vb = pick(a.v, mi) + rbase * a.vrb_in;
+    const uint8_t* sb = pick(a.s, mi) + rbase * a.srb_in;
     const int r0 = RW * (w % WPM) + grp * R;  // this group's first row of the unit's 32
     constexpr bool Q8K = Fmt<TYPE>::Q8K;
     float acc[R];
@@ -142,8 +142,8 @@ __global__ void __launch_bounds__(1024) k_fd_down(FArgs a) {
     const int e = slot < NU ? a.ids[slot] : -1;
     const long long row = e >= 0 ? (long long)e * E + i0 + i : i0 + i;
     const int mi = e >= 0 ? 2 : 5;
-    const uint8_t* vr[1] = {a.v[mi] + row * a.vrb_out};
-    const uint8_t* sr[1] = {a.s[mi] + row * a.srb_out};
+    const uint8_t* vr[1] = {pick(a.v, mi) + row * a.vrb_out};
+    const uint8_t* sr[1] = {pick(a.s, mi) + row * a.srb_out};
     constexpr bool Q8K = Fmt<TYPE>::Q8K;
     const int8_t* xq[1] = {Q8K ? a.aqk + (long long)slot * FE : a.act_q + (long long)slot * FE};
     const float* xd[1] = {Q8K ? a.adk + (long long)slot * (FE / 256) : a.act_d + (long long)slot * (FE / 32)};
@@ -216,15 +216,35 @@ size_t fa256(size_t v) { return (v + 255) & ~(size_t)255; }
 }
 
 // Scratch bytes of the three kernels for T tokens: logits, gates, quantized x, routing, the quantized down input;
-// Q4_K (T = 1) also x's activation bundle, gate / up / SwiGLU in fp32 and down's input bundle
+// Q4_K also x's activation bundle, gate / up / SwiGLU in fp32 and down's input bundle (T rows each)
 size_t moe_fused_scratch_bytes(const moe_layer_desc* d, int T) {
     const size_t NS = d->n_used + (d->s_gate ? 1 : 0), E = d->n_embd, t = T;
     size_t n = fa256(t * d->n_expert * 4) + fa256(t * 4) + fa256(t * E) + fa256(t * E / 32 * 4) +
                2 * fa256(t * 64 * 4) + fa256(t * NS * d->n_ff) + fa256(t * NS * d->n_ff / 32 * 4);
     if (d->type == QT_Q4_K)
-        n += fa256(qmatvec_q8_bytes((int)((E + 255) / 256 * 256))) + fa256(qmatvec_q8_bytes((int)(NS * d->n_ff))) +
-             3 * fa256(NS * d->n_ff * 4);
+        n += fa256(qmatvec_q8_bytes((int)(t * ((E + 255) / 256 * 256)))) +
+             fa256(qmatvec_q8_bytes((int)(t * NS * d->n_ff))) + 3 * fa256(t * NS * d->n_ff * 4);
     return n;
+}
+
+// Q4_K's pieces after the common part (a.T tokens): x's Q8_K bundle [T][E] (kernel 1), gate / up / SwiGLU in
+// fp32 [T][NS][FE] (kernel 2, then the SwiGLU kernel) and down's input bundle [T][NS][FE]; qa receives the latter
+void moe_fused_carve_q4k(FArgs& a, char* p, qmatvec_q8* qa) {
+    qmatvec_q8 qx = {};
+    const int kx = a.T * ((a.E + 255) / 256 * 256), ka = a.T * a.NS * a.FE;
+    qmatvec_q8_bind(&qx, p, kx);
+    p += fa256(qmatvec_q8_bytes(kx));
+    qmatvec_q8_bind(qa, p, ka);
+    p += fa256(qmatvec_q8_bytes(ka));
+    a.xo = {qx.q0, qx.d0, qx.qK, qx.dK, qx.bsK, qx.s0, nullptr, 0};
+    a.g = (float*)p;
+    p += fa256((size_t)ka * 4);
+    a.u = (float*)p;
+    p += fa256((size_t)ka * 4);
+    a.act = (float*)p;
+    a.aqk = qa->qK;
+    a.adk = qa->dK;
+    a.absk = qa->bsK;
 }
 
 // The scratch pieces of a.T tokens (the layout moe_fused_scratch_bytes sizes); returns the end of the common part
@@ -295,23 +315,7 @@ hipError_t moe_fused_launch(const moe_layer_desc* d, FArgs& a, void* scratch, in
     a.T = 1;
     char* p = moe_fused_carve(a, scratch);
     qmatvec_q8 qa = {};
-    if (d->type == QT_Q4_K) {  // x's bundle (kernel 1), fp32 gate / up / SwiGLU, down's input bundle
-        qmatvec_q8 qx = {};
-        const int kx = (a.E + 255) / 256 * 256, ka = a.NS * a.FE;
-        qmatvec_q8_bind(&qx, p, kx);
-        p += fa256(qmatvec_q8_bytes(kx));
-        qmatvec_q8_bind(&qa, p, ka);
-        p += fa256(qmatvec_q8_bytes(ka));
-        a.xo = {qx.q0, qx.d0, qx.qK, qx.dK, qx.bsK, qx.s0, nullptr, 0};
-        a.g = (float*)p;
-        p += fa256((size_t)ka * 4);
-        a.u = (float*)p;
-        p += fa256((size_t)ka * 4);
-        a.act = (float*)p;
-        a.aqk = qa.qK;
-        a.adk = qa.dK;
-        a.absk = qa.bsK;
-    }
+    if (d->type == QT_Q4_K) moe_fused_carve_q4k(a, p, &qa);
     int li, ni, lo, no;
     moe_mv_shape(d->type, a.E, &li, &ni);
     moe_mv_shape(d->type, a.FE, &lo, &no);

@@ -16,6 +16,7 @@
 // combine are the per-operation expressions, so the layer equals the per-operation path bit for bit.
 
 #include "fused_common.h"
+#include "gpu_ops.h"
 #include "host_common.h"
 #include "qmatvec.h"
 
@@ -25,21 +26,29 @@
 #define FM_HALVES 1  // units per round of the persistent gate / up kernel (2: halves of 8 waves, 8 rows each)
 #endif
 
-// ---- kernel 1: logits (workgroups 0 .. NE - 1), x quantized (NE .. NE + T - 1), shared gates (then T more)
+// ---- kernel 1: logits (workgroups 0 .. NE - 1), x quantized (the next nq: one per token, Q4_K one per token and
+// 256-value block, the activation quantizer itself), shared gates (then T more)
 __global__ void __launch_bounds__(256) k_fm_logits(FArgs a) {
     __shared__ float part[4];
     const int b = blockIdx.x, tid = threadIdx.x, E = a.E, T = a.T;
+    const int nq = a.xo.qK ? T * (E / 256) : T;
     stamp(a, 0);
     if (b < a.NE) {  // the per-token F32 matvec's sums, one token after the other
         for (int t = 0; t < T; ++t) {
             const float y = f32_row_dot(a.w_router + (size_t)b * E, a.x + (size_t)t * E, E, part);
             if (tid == 0) a.logits[(size_t)t * a.NE + b] = y;
         }
-    } else if (b < a.NE + T) {
-        const int t = b - a.NE;
-        quantize_row_q8_0(a.x + (size_t)t * E, E, a.xq + (size_t)t * E, a.xd + (size_t)t * (E / 32));
+    } else if (b < a.NE + nq) {
+        if (a.xo.qK) {  // block blk of the [T][E] bundle: token blk / (E / 256)
+            __shared__ Q8Smem sh;
+            const int blk = b - a.NE;
+            q8_quantize_256(a.x[(size_t)blk * 256 + tid], true, blk, tid, sh, a.xo);
+        } else {
+            const int t = b - a.NE;
+            quantize_row_q8_0(a.x + (size_t)t * E, E, a.xq + (size_t)t * E, a.xd + (size_t)t * (E / 32));
+        }
     } else {
-        const int t = b - a.NE - T;
+        const int t = b - a.NE - nq;
         const float g = shexp_gate(a.x + (size_t)t * E, a.w_shexp, E, part);
         if (tid == 0) a.sg[t] = g;
     }
@@ -75,24 +84,44 @@ __device__ __forceinline__ int slot_of(const int* ids_t, int nu, int e) {
 // units (union slot, 32-row block of FE) two at a time (one per half of the workgroup: 4 waves of 8 gate rows, 4 of
 // 8 up rows; one at a time over 16 waves of 4 rows when a lane holds two units of a row), the unit's weights
 // loaded once and dotted with every token that chose the slot's expert, then those tokens' SwiGLU and Q8_0 blocks
-// of down's input
-template <int TYPE, int NUPL_IN>
+// of down's input. A row is one group of L_IN lanes with NUPL_IN units per lane (the per-operation shape for
+// K = E), so a wave holds 64 / L_IN groups of RW L_IN / 64 rows. Q4_K writes gate / up in fp32 instead (its down
+// input is Q8_K, one scale per 256 values: the SwiGLU kernel between kernels 2 and 3 quantizes it).
+template <int TYPE, int L_IN, int NUPL_IN>
 __global__ void __launch_bounds__(1024) k_fm_gate_up(FArgs a) {
     // NUPL_IN == 1: two units at a time (halves of 8 waves, 8 rows per wave); 2: one unit (16 waves, 4 rows)
-    constexpr int HALVES = FM_HALVES, WPU = 16 / HALVES, RW = 64 / WPU, WPM = 32 / RW, TB = NUPL_IN == 1 ? 2 : 1;
+    constexpr int HALVES = FM_HALVES, WPU = 16 / HALVES, RW = 64 / WPU, WPM = 32 / RW;
+    constexpr int TB = NUPL_IN == 1 ? 2 : 1, G = 64 / L_IN, R = RW / G;  // lane groups per wave, rows per group
+    static_assert(R >= 1, "a wave's rows must cover its lane groups");
+    constexpr bool Q8K = Fmt<TYPE>::Q8K;
     __shared__ int s_ids[FD_MAX_T][64];
     __shared__ float s_wts[FD_MAX_T][64];
     __shared__ uint32_t bits[ROUTER_MAX_E / 32];
     __shared__ int ulist[FM_MAX_U], s_nu;
     __shared__ int s_slot[2][FD_MAX_T];
     __shared__ float gu[2][2][FD_MAX_T][32];  // [half][gate / up][token][row]
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // every token's quantized x, staged once: Q8_0 values [T][E] and scales [T][E / 32], or Q8_K values, scales
+    // [T][E / 256] and sums of 16 [T][E / 16]
+    __shared__ __align__(16) int8_t s_xq[FD_MAX_T * FD_MAX_E];
+    __shared__ float s_xd[FD_MAX_T * FD_MAX_E / 32];
+    __shared__ __align__(16) int s_xbs[Q8K ? FD_MAX_T * FD_MAX_E / 16 : 4];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, gl = lane & (L_IN - 1), grp = lane / L_IN;
     const int h = w / WPU, hw = w - h * WPU;  // unit of the round, wave within it
     const int T = a.T, FE = a.FE, NU = a.NU, NE = a.NE, nbf = FE / 32, nu_in = fmt_units(TYPE, a.E);
     stamp(a, 2);
     for (int i = tid; i < (NE + 31) / 32; i += 1024) bits[i] = 0u;
     const float* lg = a.logits_in ? a.logits_in : a.logits;
-    if (w < T) router_select_one_wave(lg + (size_t)w * NE, NE, NU, s_ids[w], s_wts[w]);
+    if (w < T) {
+        router_select_one_wave(lg + (size_t)w * NE, NE, NU, s_ids[w], s_wts[w]);
+    } else {  // the other waves stage x meanwhile
+        const int i0 = tid - 64 * T, n = 1024 - 64 * T, TE = T * a.E;
+        const int8_t* gq = Q8K ? a.xo.qK : a.xq;
+        const float* gd = Q8K ? a.xo.dK : a.xd;
+        for (int i = i0; i < TE / 16; i += n) ((uint4*)s_xq)[i] = ((const uint4*)gq)[i];
+        for (int i = i0; i < TE / (Q8K ? 256 : 32); i += n) s_xd[i] = gd[i];
+        if constexpr (Q8K)
+            for (int i = i0; i < TE / 64; i += n) ((int4*)s_xbs)[i] = ((const int4*)a.xo.bsK)[i];
+    }
     __syncthreads();
     if (tid < T * NU) {
         const int t = tid / NU, j = tid - t * NU;
@@ -116,22 +145,22 @@ __global__ void __launch_bounds__(1024) k_fm_gate_up(FArgs a) {
     __syncthreads();
     stamp(a, 3);
     const int units = s_nu * nbf, step = HALVES * gridDim.x;
-    const int mat = hw / WPM;
-    // this wave's weight units of unit k (RW rows of gate or up): issued a round ahead of their use
-    auto load_w = [&](int k, WUnit<TYPE> (&wu)[NUPL_IN][RW]) {
+    const int mat = hw / WPM, r0 = RW * (hw % WPM) + grp * R;  // gate or up; this group's first row of the unit's 32
+    // this group's weight units of unit k (R rows of gate or up): issued a round ahead of their use
+    auto load_w = [&](int k, WUnit<TYPE> (&wu)[NUPL_IN][R]) {
         const int u = k / nbf, b = k - u * nbf, e = ulist[u];
         const int mi = e >= 0 ? mat : 3 + mat;
-        const long long rbase = (e >= 0 ? (long long)e * FE : 0) + 32 * b + RW * (hw % WPM);
-        const uint8_t* vb = a.v[mi] + rbase * a.vrb_in;
-        const uint8_t* sb = a.s[mi] + rbase * a.srb_in;
+        const long long rbase = (e >= 0 ? (long long)e * FE : 0) + 32 * b + r0;
+        const uint8_t* vb = pick(a.v, mi) + rbase * a.vrb_in;
+        const uint8_t* sb = pick(a.s, mi) + rbase * a.srb_in;
 #pragma unroll
         for (int i = 0; i < NUPL_IN; ++i)
 #pragma unroll
-            for (int r = 0; r < RW; ++r)
-                load_unit<TYPE, true>(vb + (long long)r * a.vrb_in, sb + (long long)r * a.srb_in, lane + i * 64,
+            for (int r = 0; r < R; ++r)
+                load_unit<TYPE, true>(vb + (long long)r * a.vrb_in, sb + (long long)r * a.srb_in, gl + i * L_IN,
                                       nu_in, wu[i][r]);
     };
-    WUnit<TYPE> wu[NUPL_IN][RW];
+    WUnit<TYPE> wu[NUPL_IN][R];
     if (HALVES * blockIdx.x + h < units) load_w(HALVES * blockIdx.x + h, wu);
     for (int k0 = HALVES * blockIdx.x; k0 < units; k0 += step) {  // (uniform over the workgroup)
         const int unit = k0 + h;
@@ -147,34 +176,45 @@ __global__ void __launch_bounds__(1024) k_fm_gate_up(FArgs a) {
 #pragma unroll
                 for (int q = 0; q < TB; ++q) {  // the batch's participating tokens' x, issued together
                     const int t = t0 + q;
-                    if (t < T && s_slot[h][t] >= 0)
+                    if (!Q8K && t < T && s_slot[h][t] >= 0)  // (Q8_K: one unit at a time, below)
 #pragma unroll
                         for (int i = 0; i < NUPL_IN; ++i)
-                            load_x<TYPE>(a.xq + (size_t)t * a.E, a.xd + (size_t)t * (a.E / 32), nullptr,
-                                         lane + i * 64, x[q][i]);
+                            load_x<TYPE>(s_xq + t * a.E, s_xd + t * (a.E / 32), nullptr, gl + i * L_IN, x[q][i]);
                 }
 #pragma unroll
                 for (int q = 0; q < TB; ++q) {
                     const int t = t0 + q;
                     if (t >= T || s_slot[h][t] < 0) continue;  // (uniform)
-                    float acc[RW];
+                    float acc[R];
 #pragma unroll
-                    for (int r = 0; r < RW; ++r) {
-                        acc[r] = 0.0f;
+                    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 #pragma unroll
-                        for (int i = 0; i < NUPL_IN; ++i) acc[r] += term<TYPE>(wu[i][r], x[q][i], lane + i * 64);
-                        acc[r] = group_sum<64>(acc[r]);
+                    for (int i = 0; i < NUPL_IN; ++i) {
+                        if constexpr (Q8K)  // (the 128 VGPRs of a 1024-thread workgroup hold one Q8_K unit)
+                            load_x<TYPE>(s_xq + t * a.E, s_xd + t * (a.E / 256), s_xbs + t * (a.E / 16),
+                                         gl + i * L_IN, x[q][i]);
+#pragma unroll
+                        for (int r = 0; r < R; ++r) acc[r] += term<TYPE>(wu[i][r], x[q][i], gl + i * L_IN);
                     }
-                    if (lane == 0)
 #pragma unroll
-                        for (int r = 0; r < RW; ++r) gu[h][mat][t][RW * (hw % WPM) + r] = acc[r];
+                    for (int r = 0; r < R; ++r) acc[r] = group_sum<L_IN>(acc[r]);
+                    if (gl == 0) {
+                        if constexpr (Q8K) {  // row (token t, its slot of e) of the fp32 gate / up
+                            float* o = (mat ? a.u : a.g) + ((long long)t * a.NS + s_slot[h][t]) * FE + 32 * b + r0;
+#pragma unroll
+                            for (int r = 0; r < R; ++r) o[r] = acc[r];
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < R; ++r) gu[h][mat][t][r0 + r] = acc[r];
+                        }
+                    }
                 }
             }
         }
         if (unit + step < units) load_w(unit + step, wu);  // the next round's weights, in flight from here on
         __syncthreads();
         stamp(a, 7);
-        if (live && hw < T && s_slot[h][hw] >= 0) {  // token hw's SwiGLU and Q8_0 block for its slot of e
+        if (!Q8K && live && hw < T && s_slot[h][hw] >= 0) {  // token hw's SwiGLU and Q8_0 block for its slot of e
             const long long sl = (long long)hw * a.NS + s_slot[h][hw];
             swiglu_q8_block(gu[h][0][hw], gu[h][1][hw], a.act_q + sl * FE + 32 * b, a.act_d + sl * nbf + b);
         }
@@ -187,7 +227,7 @@ __global__ void __launch_bounds__(1024) k_fm_gate_up(FArgs a) {
 // combine kernel's expression)
 template <int TYPE, int L_OUT, int NUPL_OUT>
 __global__ void __launch_bounds__(1024) k_fm_down(FArgs a) {
-    constexpr int RB = 64 / L_OUT, IB = NUPL_OUT == 1 ? 4 : 2;
+    constexpr int RB = 64 / L_OUT, IB = NUPL_OUT == 1 && !Fmt<TYPE>::Q8K ? 4 : 2;  // (128 VGPRs at 1024 threads)
     __shared__ int s_e[FD_MAX_T * 17];
     __shared__ float s_wts[FD_MAX_T][64];
     __shared__ float downv[FD_MAX_T][17][RB];
@@ -212,14 +252,19 @@ __global__ void __launch_bounds__(1024) k_fm_down(FArgs a) {
                 const int e = s_e[k];
                 const long long row = e >= 0 ? (long long)e * E + i0 + i : i0 + i;
                 const int mi = e >= 0 ? 2 : 5;
-                const uint8_t* vr = a.v[mi] + row * a.vrb_out;
-                const uint8_t* sr = a.s[mi] + row * a.srb_out;
+                const uint8_t* vr = pick(a.v, mi) + row * a.vrb_out;
+                const uint8_t* sr = pick(a.s, mi) + row * a.srb_out;
 #pragma unroll
                 for (int c = 0; c < NUPL_OUT; ++c) load_packed<TYPE>(vr, sr, gl + c * L_OUT, nu_out, wu[q][c]);
 #pragma unroll
-                for (int c = 0; c < NUPL_OUT; ++c)
-                    load_x<TYPE>(a.act_q + (long long)k * FE, a.act_d + (long long)k * (FE / 32), nullptr,
-                                 gl + c * L_OUT, x[q][c]);
+                for (int c = 0; c < NUPL_OUT; ++c) {
+                    if constexpr (Fmt<TYPE>::Q8K)
+                        load_x<TYPE>(a.aqk + (long long)k * FE, a.adk + (long long)k * (FE / 256),
+                                     a.absk + (long long)k * (FE / 16), gl + c * L_OUT, x[q][c]);
+                    else
+                        load_x<TYPE>(a.act_q + (long long)k * FE, a.act_d + (long long)k * (FE / 32), nullptr,
+                                     gl + c * L_OUT, x[q][c]);
+                }
             }
         }
 #pragma unroll
@@ -249,36 +294,50 @@ __global__ void __launch_bounds__(1024) k_fm_down(FArgs a) {
 
 namespace {
 
-template <int TYPE, int NI, int LO, int NO>
-hipError_t launch_multi(const FArgs& a, int kernels, hipStream_t st) {
+template <int TYPE, int LI, int NI, int LO, int NO>
+hipError_t launch_multi(const FArgs& a, const qmatvec_q8* qa, int kernels, hipStream_t st) {
     const int nsu = (a.T * a.NU < a.NE ? a.T * a.NU : a.NE) + (a.NS > a.NU ? 1 : 0);  // union slots, at most
     const int per = FM_HALVES;                                                        // units per round
     const int pairs = (nsu * (a.FE / 32) + per - 1) / per, cus = moe_device_cus();
     hipError_t e = hipSuccess;
-    if (kernels & 1) e = launch_kernel(k_fm_logits, dim3(a.NE + a.T * (1 + a.has_gate)), dim3(256), 0, st, a);
+    const int nq = Fmt<TYPE>::Q8K ? a.T * (a.E / 256) : a.T;  // quantizing workgroups of kernel 1
+    if (kernels & 1) e = launch_kernel(k_fm_logits, dim3(a.NE + nq + a.T * a.has_gate), dim3(256), 0, st, a);
     if (e == hipSuccess && (kernels & 2))
-        e = launch_kernel(k_fm_gate_up<TYPE, NI>, dim3(pairs < cus ? pairs : cus), dim3(1024), 0, st, a);
+        e = launch_kernel(k_fm_gate_up<TYPE, LI, NI>, dim3(pairs < cus ? pairs : cus), dim3(1024), 0, st, a);
+    if (Fmt<TYPE>::Q8K && e == hipSuccess && (kernels & 2))
+        e = gpu_swiglu(a.g, a.u, a.act, a.T * a.NS * a.FE, qa, st);
     if (e == hipSuccess && (kernels & 4))
         e = launch_kernel(k_fm_down<TYPE, LO, NO>, dim3(a.E / (64 / LO)), dim3(1024), 0, st, a);
     return e;
 }
 
 template <int TYPE>
-hipError_t launch_multi_t(const FArgs& a, int ni, int lo, int no, int kernels, hipStream_t st) {
+hipError_t launch_multi_t(const FArgs& a, const qmatvec_q8* qa, int li, int ni, int lo, int no, int kernels,
+                          hipStream_t st) {
 #define FM_CASE(I, L, O) \
-    if (ni == I && lo == L && no == O) return launch_multi<TYPE, I, L, O>(a, kernels, st);
-    FM_CASE(1, 16, 1) FM_CASE(1, 8, 3) FM_CASE(1, 32, 1) FM_CASE(1, 16, 3) FM_CASE(1, 64, 1)
-    FM_CASE(2, 16, 1) FM_CASE(2, 8, 3) FM_CASE(2, 32, 1) FM_CASE(2, 16, 3) FM_CASE(2, 64, 1)
+    if (li == 64 && ni == I && lo == L && no == O) return launch_multi<TYPE, 64, I, L, O>(a, qa, kernels, st);
+    if constexpr (TYPE == QT_Q4_K) {
+        if (li == 16 && ni == 3 && lo == 16 && no == 1) return launch_multi<TYPE, 16, 3, 16, 1>(a, qa, kernels, st);
+    } else {
+        FM_CASE(1, 16, 1) FM_CASE(1, 8, 3) FM_CASE(1, 32, 1) FM_CASE(1, 16, 3) FM_CASE(1, 64, 1)
+        FM_CASE(2, 16, 1) FM_CASE(2, 8, 3) FM_CASE(2, 32, 1) FM_CASE(2, 16, 3) FM_CASE(2, 64, 1)
+    }
 #undef FM_CASE
     return hipErrorInvalidDeviceFunction;
 }
 
 }  // namespace
 
+static bool g_fm_q4k = false;  // Q4_K through the multi-token kernels (the parity tests turn it on)
+extern "C" void moe_layer_fused_multi_q4k(int on) { g_fm_q4k = on != 0; }
+
 // T = 2..FD_MAX_T tokens through the multi-token kernels, when moe_fused_prepare takes the layer
 bool moe_fused_multi_try(const moe_layer_desc* d, const float* x, const float* logits, int T, float* out,
                          int* ids_out, float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err) {
-    if (T < 2 || T > FD_MAX_T || d->type == QT_Q4_K) return false;  // (Q4_K: the per-operation path)
+    // Q4_K: the per-operation path. These kernels are bit-exact for it, but with 256 experts few rows are shared
+    // between tokens and the per-operation id-batch launches read the rows faster (config-3 shape, T = 4: 55.5 us
+    // against 71 us per layer).
+    if (T < 2 || T > FD_MAX_T || (d->type == QT_Q4_K && !g_fm_q4k)) return false;
     FArgs a = {};
     if (!moe_fused_prepare(d, a)) return false;
     if (a.NS > 17 || T * a.NU > 64) return false;  // (the union and the per-token slot tables' sizes)
@@ -289,14 +348,17 @@ bool moe_fused_multi_try(const moe_layer_desc* d, const float* x, const float* l
     a.ids_out = ids_out;
     a.wts_out = wts_out;
     a.stamps = moe_fused_stamps_ptr();
-    moe_fused_carve(a, scratch);
+    char* p = moe_fused_carve(a, scratch);
+    qmatvec_q8 qa = {};
+    if (d->type == QT_Q4_K) moe_fused_carve_q4k(a, p, &qa);
     int li, ni, lo, no;
     moe_mv_shape(d->type, a.E, &li, &ni);
     moe_mv_shape(d->type, a.FE, &lo, &no);
     switch (d->type) {
-    case QT_Q8_0: *err = launch_multi_t<QT_Q8_0>(a, ni, lo, no, kernels, st); break;
-    case QT_ROCMFP4: *err = launch_multi_t<QT_ROCMFP4>(a, ni, lo, no, kernels, st); break;
-    default: *err = launch_multi_t<QT_ROCMFP4_FAST>(a, ni, lo, no, kernels, st); break;
+    case QT_Q8_0: *err = launch_multi_t<QT_Q8_0>(a, &qa, li, ni, lo, no, kernels, st); break;
+    case QT_ROCMFP4: *err = launch_multi_t<QT_ROCMFP4>(a, &qa, li, ni, lo, no, kernels, st); break;
+    case QT_ROCMFP4_FAST: *err = launch_multi_t<QT_ROCMFP4_FAST>(a, &qa, li, ni, lo, no, kernels, st); break;
+    default: *err = launch_multi_t<QT_Q4_K>(a, &qa, li, ni, lo, no, kernels, st); break;
     }
     return true;
 }

@@ -32,6 +32,17 @@ struct Q8Out {
     int xh_bf16;
 };
 
+// p[i] for a run-time i of a kernel-argument array, as a chain of selects over its elements (which arrive with the
+// other arguments in scalar registers). Indexing the array itself becomes a vector load from the argument segment:
+// one more memory round trip ahead of every load whose address depends on it.
+template <int N, typename T>
+__device__ __forceinline__ T pick(const T (&p)[N], int i) {
+    T r = p[0];
+#pragma unroll
+    for (int k = 1; k < N; ++k) r = i == k ? p[k] : r;
+    return r;
+}
+
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
 // UE4M3 scale byte at half scale: (8 + m) 2^(e - 11), subnormals m 2^-10, 0x7f and above 0
