@@ -132,12 +132,16 @@ __device__ __forceinline__ void quantize_row_q8_0(const float* x, int E, int8_t*
     for (int base = 0; base < E; base += 2048) {
         const int i0 = base + 8 * tid;
         float v[8];
+        if (i0 + 8 <= E && ((uintptr_t)(x + i0) & 15) == 0) {  // two 16-byte loads
+            const float4 p = ((const float4*)(x + i0))[0], q = ((const float4*)(x + i0))[1];
+            v[0] = p.x, v[1] = p.y, v[2] = p.z, v[3] = p.w, v[4] = q.x, v[5] = q.y, v[6] = q.z, v[7] = q.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = i0 + j < E ? x[i0 + j] : 0.0f;
+        }
         float am = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            v[j] = i0 + j < E ? x[i0 + j] : 0.0f;
-            am = fmaxf(am, fabsf(v[j]));
-        }
+        for (int j = 0; j < 8; ++j) am = fmaxf(am, fabsf(v[j]));
         am = group_max<4>(am);
         const float id = am != 0.0f ? 127.0f / am : 0.0f;
         if (i0 < E) {
