@@ -209,6 +209,63 @@ __global__ void __launch_bounds__(256) k_matmul_f32(const float* W, long long ld
             if (t0 + tt + i < T && r0 + tr + j < N) Y[(size_t)(t0 + tt + i) * N + r0 + tr + j] = acc[i][j];
 }
 
+// Prefill on fp32 MFMA (v_mfma_f32_32x32x2f32, exact fp32 products): one 32-token x 32-row output tile per
+// workgroup, its MF_KS waves each 1 / MF_KS of K (more waves in flight to cover the loads' latency), summed through
+// LDS in a fixed order. Both operands are rows along K, so lane l reads 16 consecutive values (64 bytes) of token /
+// weight row l % 32 per 32-value chunk (its half l / 32 of the chunk), and MFMA q of the chunk pairs value q of both
+// lanes' runs: k = chunk + 16 h + q on both sides. The next chunk's loads are issued before the current chunk's 16
+// MFMAs. K % (32 MF_KS) == 0.
+// Workgroups go to the 8 XCDs in turn (linear id L on XCD L % 8), so the grid is one-dimensional and L = 8 j + c
+// takes token tile 8 (j / nx) + c, row tile j % nx: the nx workgroups of a token tile share one XCD's L2, which
+// then fetches the tile's 32 token rows once (a row tile per grid column had spread them over all 8).
+typedef float mf_v16f __attribute__((ext_vector_type(16)));
+#ifndef MF_KS
+#define MF_KS 8
+#endif
+__global__ void __launch_bounds__(64 * MF_KS) k_matmul_f32_mfma(const float* W, long long ldw, const float* X,
+                                                               float* Y, int N, int K, int T) {
+    __shared__ float red[MF_KS - 1][16][64];
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, h = l >> 5;
+    const int nx = (N + 31) / 32, xc = blockIdx.x & 7, j = blockIdx.x >> 3;
+    const int r0 = (j % nx) * 32, t0 = (8 * (j / nx) + xc) * 32;
+    if (t0 >= T) return;  // (the last round of token tiles on some XCDs; uniform)
+    const int kq = K / MF_KS, kb = w * kq;  // this wave's share of K
+    const float* xr = X + (size_t)min(t0 + (l & 31), T - 1) * K + kb + 16 * h;  // (rows past the end: the last
+    const float* wr = W + (size_t)min(r0 + (l & 31), N - 1) * ldw + kb + 16 * h;  //  row, results unused)
+    float4 xa[4], wa[4], xn[4], wn[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xa[q] = ((const float4*)xr)[q], wa[q] = ((const float4*)wr)[q];
+    mf_v16f acc = {};
+    for (int c = 32; c <= kq; c += 32) {
+        if (c < kq)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) xn[q] = ((const float4*)(xr + c))[q], wn[q] = ((const float4*)(wr + c))[q];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[q].x, wa[q].x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[q].y, wa[q].y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[q].z, wa[q].z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[q].w, wa[q].w, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xa[q] = xn[q], wa[q] = wn[q];
+    }
+    if (w > 0)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) red[w - 1][i][l] = acc[i];
+    __syncthreads();
+    if (w == 0) {  // acc[i]: token 8 (i / 4) + 4 h + i % 4, row l % 32 of the tile
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float v = acc[i];
+#pragma unroll
+            for (int q = 0; q < MF_KS - 1; ++q) v += red[q][i][l];
+            const int t = t0 + 8 * (i >> 2) + 4 * h + (i & 3), r = r0 + (l & 31);
+            if (t < T && r < N) Y[(size_t)t * N + r] = v;
+        }
+    }
+}
+
 // ------------------------------------------------------------------ router (src/gpu_ops.hip:185-241)
 
 // One 256-thread workgroup per token: the shared-expert gate, then router_select (router_dev.h).
@@ -276,6 +333,9 @@ extern "C" hipError_t qmatvec_launch_batch(int type, const void* W, size_t row_b
     if (N <= 0 || K <= 0 || T <= 0 || row_bytes != (size_t)K * 4) return hipErrorInvalidValue;
     if (T <= 16)  // a few tokens: the decode kernel per token (the same sums as T single-token launches)
         return launch_kernel(k_matvec_f32, dim3(N, T), dim3(256), 0, stream, (const float*)W, (long long)K, x, y, N, K);
+    if (K % (32 * MF_KS) == 0 && (((uintptr_t)W | (uintptr_t)x) & 15) == 0)
+        return launch_kernel(k_matmul_f32_mfma, dim3(8 * ((N + 31) / 32) * ((T + 255) / 256)), dim3(64 * MF_KS), 0,
+                             stream, (const float*)W, (long long)K, x, y, N, K, T);
     return launch_kernel(k_matmul_f32, dim3((N + MF_TR - 1) / MF_TR, (T + MF_TT - 1) / MF_TT), dim3(256), 0, stream,
                          (const float*)W, (long long)K, x, y, N, K, T);
 }
