@@ -88,7 +88,7 @@ struct GArgs {
 #define GG_TILE 64  // entries per tile (64 or 128: two or four 32-entry MFMA tiles per wave)
 #endif
 #ifndef GG_KB
-#define GG_KB 8  // blocks of 32 values per stage (4 or 8)
+#define GG_KB 4  // blocks of 32 values per stage (4 or 8; 4 keeps the down kernels at 4-5 waves per SIMD)
 #endif
 #ifndef GG_KB2
 #define GG_KB2 4  // the same for the gate / up / SwiGLU kernel (two matrices per stage)
@@ -322,7 +322,14 @@ __device__ __forceinline__ void h_compute(const HBuf<NM, KB>& B, const uint4 (&w
 // act = SiLU(g) u (the swiglu kernel's expression) and its Q8_0 blocks -- a wave's 32 rows of one entry are one
 // block: 16 values in each of lanes l and l + 32 -- into a.aq / a.ad (the quantizer's expressions).
 template <int TYPE, int NM, int KB>
-__global__ void __launch_bounds__(256) k_grouped(GArgs a) {
+#ifndef GG_WPE
+#define GG_WPE 3  // waves per SIMD asked of the compiler (0: its choice; 3 measured 3-8% faster than its 2)
+#endif
+__global__ void __launch_bounds__(256)
+#if GG_WPE
+__attribute__((amdgpu_waves_per_eu(GG_WPE)))
+#endif
+k_grouped(GArgs a) {
     __shared__ __attribute__((aligned(1024))) typename BufOf<TYPE, NM, KB>::type buf;
     constexpr bool F16 = TYPE != QT_Q8_0;
     const int k = blockIdx.y;
