@@ -94,6 +94,7 @@ bool moe_fused_prepare(const moe_layer_desc* d, FArgs& a);
 size_t moe_fused_scratch_bytes(const moe_layer_desc* d, int T);
 char* moe_fused_carve(FArgs& a, void* scratch);
 void moe_fused_carve_q4k(FArgs& a, char* p, qmatvec_q8* qa);  // Q4_K's pieces, from the common part's end
+hipError_t moe_fused_launch_down(int type, const FArgs& a, hipStream_t st);  // kernel 3 for a.T tokens
 void moe_mv_shape(int type, int K, int* lanes, int* units_per_lane);
 unsigned long long* moe_fused_stamps_ptr();  // the table moe_layer_fused_stamps set, or nullptr
 

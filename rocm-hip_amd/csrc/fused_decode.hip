@@ -130,34 +130,36 @@ __global__ void __launch_bounds__(64 * (64 / FD_GU_RW)) k_fd_gate_up(FArgs a) {
 
 // ---- kernel 3: down rows of every slot for RB = 64 / L_OUT output rows, then the combine in slot order. One wave
 // per slot, one lane group of L_OUT lanes (NUPL_OUT units each) per output row: the per-operation down kernel's
-// shape for this K, so the same sums.
+// shape for this K, so the same sums. Token blockIdx.y (T = 1: 0; the multi-token layer launches T rows of
+// workgroups over the same row blocks).
 template <int TYPE, int L_OUT, int NUPL_OUT>
 __global__ void __launch_bounds__(1024) k_fd_down(FArgs a) {
     constexpr int RB = 64 / L_OUT;
     __shared__ float downv[16][RB];
-    const int tid = threadIdx.x, E = a.E, FE = a.FE, NU = a.NU, NS = a.NS;
+    const int tid = threadIdx.x, E = a.E, FE = a.FE, NU = a.NU, NS = a.NS, t = blockIdx.y;
     const int slot = tid >> 6, lane = tid & 63, gl = lane & (L_OUT - 1), i = lane / L_OUT;
     const int i0 = blockIdx.x * RB;
     stamp(a, 5);
-    const int e = slot < NU ? a.ids[slot] : -1;
+    const int e = slot < NU ? a.ids[t * NU + slot] : -1;
     const long long row = e >= 0 ? (long long)e * E + i0 + i : i0 + i;
     const int mi = e >= 0 ? 2 : 5;
     const uint8_t* vr[1] = {pick(a.v, mi) + row * a.vrb_out};
     const uint8_t* sr[1] = {pick(a.s, mi) + row * a.srb_out};
     constexpr bool Q8K = Fmt<TYPE>::Q8K;
-    const int8_t* xq[1] = {Q8K ? a.aqk + (long long)slot * FE : a.act_q + (long long)slot * FE};
-    const float* xd[1] = {Q8K ? a.adk + (long long)slot * (FE / 256) : a.act_d + (long long)slot * (FE / 32)};
-    const int* xbs[1] = {Q8K ? a.absk + (long long)slot * (FE / 16) : nullptr};
+    const long long sl = (long long)t * NS + slot;  // this (token, slot) pair's row of down's input
+    const int8_t* xq[1] = {Q8K ? a.aqk + sl * FE : a.act_q + sl * FE};
+    const float* xd[1] = {Q8K ? a.adk + sl * (FE / 256) : a.act_d + sl * (FE / 32)};
+    const int* xbs[1] = {Q8K ? a.absk + sl * (FE / 16) : nullptr};
     float acc[1];
     rows_dot_multi<TYPE, L_OUT, 1, NUPL_OUT>(vr, sr, xq, xd, xbs, fmt_units(TYPE, FE), gl, 1, acc);
     if (gl == 0) downv[slot][i] = acc[0];
     __syncthreads();
     if (tid < RB) {  // the combine kernel's expression
-        const float* wts = a.wts;
+        const float* wts = a.wts + t * NU;
         float o = wts[0] * downv[0][tid];
         for (int j = 1; j < NU; ++j) o += wts[j] * downv[j][tid];
-        if (NS > NU) o += a.has_gate ? downv[NU][tid] * a.sg[0] : downv[NU][tid];
-        a.out[i0 + tid] = o;
+        if (NS > NU) o += a.has_gate ? downv[NU][tid] * a.sg[t] : downv[NU][tid];
+        a.out[(size_t)t * E + i0 + tid] = o;
     }
     stamp(a, 6);
 }
@@ -199,6 +201,20 @@ hipError_t launch_fused_t(const FArgs& a, const qmatvec_q8* qa, int li, int ni, 
         FD_CASE(2, 16, 1) FD_CASE(2, 8, 3) FD_CASE(2, 32, 1) FD_CASE(2, 16, 3) FD_CASE(2, 64, 1)
     }
 #undef FD_CASE
+    return hipErrorInvalidDeviceFunction;
+}
+
+template <int TYPE>
+hipError_t launch_down_t(const FArgs& a, int lo, int no, hipStream_t st) {
+    const dim3 g(a.E / (64 / lo), a.T), b(64 * a.NS);
+#define FD_DOWN(L, O) \
+    if (lo == L && no == O) return launch_kernel(k_fd_down<TYPE, L, O>, g, b, 0, st, a);
+    if constexpr (TYPE == QT_Q4_K) {
+        FD_DOWN(16, 1)
+    } else {
+        FD_DOWN(16, 1) FD_DOWN(8, 3) FD_DOWN(32, 1) FD_DOWN(16, 3) FD_DOWN(64, 1)
+    }
+#undef FD_DOWN
     return hipErrorInvalidDeviceFunction;
 }
 
@@ -324,6 +340,18 @@ hipError_t moe_fused_launch(const moe_layer_desc* d, FArgs& a, void* scratch, in
     case QT_ROCMFP4: return launch_fused_t<QT_ROCMFP4>(a, &qa, li, ni, lo, no, kernels, st);
     case QT_ROCMFP4_FAST: return launch_fused_t<QT_ROCMFP4_FAST>(a, &qa, li, ni, lo, no, kernels, st);
     default: return launch_fused_t<QT_Q4_K>(a, &qa, li, ni, lo, no, kernels, st);
+    }
+}
+
+// Kernel 3 for a.T tokens (grid: row blocks x tokens), the multi-token layer's down + combine
+hipError_t moe_fused_launch_down(int type, const FArgs& a, hipStream_t st) {
+    int lo, no;
+    moe_mv_shape(type, a.FE, &lo, &no);
+    switch (type) {
+    case QT_Q8_0: return launch_down_t<QT_Q8_0>(a, lo, no, st);
+    case QT_ROCMFP4: return launch_down_t<QT_ROCMFP4>(a, lo, no, st);
+    case QT_ROCMFP4_FAST: return launch_down_t<QT_ROCMFP4_FAST>(a, lo, no, st);
+    default: return launch_down_t<QT_Q4_K>(a, lo, no, st);
     }
 }
 

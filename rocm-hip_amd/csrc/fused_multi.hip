@@ -5,13 +5,15 @@
 // reference's moe_core for T < 8, src/qwen_model.cpp:904-937). Here:
 //   1  one workgroup per router-logit row (every token's dot with it), one per token quantizing x, one per token
 //      for the shared-expert gate;
-//   2  a persistent workgroup per CU: it routes all T tokens (wave t routes token t, the router's own code) and
-//      forms the union of the chosen experts in ascending expert order (then the shared expert) once, then takes
-//      units (union slot, 32-row block of FE) two at a time: the slot expert's 32 gate and 32 up rows against
-//      each token that chose it, then each such token's SwiGLU and Q8_0 block of down's input; workgroup 0
-//      publishes the routing;
-//   3  one workgroup per 64 / L output rows (L: the down row dot's lanes): the (token, slot) pairs' down rows,
-//      then the combine per token in slot order.
+//   2  gate / up / SwiGLU over units (union slot, 32-row block of FE), the union being the chosen experts in
+//      ascending order (then the shared expert): each unit's rows are dotted with every token that chose the
+//      slot's expert, then each such token's SwiGLU and Q8_0 block of down's input. Two forms: a workgroup per
+//      unit (every workgroup routes all T tokens, one wave each, and forms the union itself) when the grid fits
+//      one round of resident workgroups; otherwise a persistent workgroup per CU that routes once and takes
+//      units round after round;
+//   3  down + combine: per token (the T = 1 kernel, one wave per slot, over T rows of workgroups), or the
+//      item-list form (one workgroup per 64 / L output rows takes every (token, slot) pair, then combines per
+//      token in slot order).
 // Each row dot has the per-operation kernel's lane shape and order for its K, the router, quantizer, SwiGLU and
 // combine are the per-operation expressions, so the layer equals the per-operation path bit for bit.
 
@@ -222,6 +224,125 @@ __global__ void __launch_bounds__(1024) k_fm_gate_up(FArgs a) {
     stamp(a, 4);
 }
 
+// ---- kernel 2, one workgroup per unit (union slot, 32-row block of FE), the grid sized for the largest union:
+// every workgroup routes all T tokens (wave t routes token t) while its other waves stage every token's quantized
+// x in LDS, forms the union (routed experts ascending, then the shared one) and leaves when its unit is past the
+// union's end; then 8 waves of 8 rows (4 waves of gate rows, 4 of up) of the slot expert, all loaded at once and
+// dotted with each token that chose the expert, then those tokens' SwiGLU and Q8_0 blocks of down's input (Q4_K:
+// fp32 gate / up for the SwiGLU kernel). The workgroups of a launch load their units together, instead of a
+// persistent workgroup's units one round (and one memory latency) after the other.
+template <int TYPE, int L_IN, int NUPL_IN>
+__global__ void __launch_bounds__(512) k_fm_gate_up_unit(FArgs a) {
+    constexpr int RW = 8, WPM = 4;            // rows per wave, waves per matrix
+    constexpr int G = 64 / L_IN, R = RW / G;  // lane groups per wave, rows per group
+    static_assert(R >= 1, "a wave's rows must cover its lane groups");
+    constexpr bool Q8K = Fmt<TYPE>::Q8K;
+    __shared__ int s_ids[FD_MAX_T][64];
+    __shared__ float s_wts[FD_MAX_T][64];
+    __shared__ uint32_t bits[ROUTER_MAX_E / 32];
+    __shared__ int ulist[FM_MAX_U], s_nu;
+    __shared__ int s_slot[FD_MAX_T];
+    __shared__ float gu[2][FD_MAX_T][32];  // [gate / up][token][row]
+    __shared__ __align__(16) int8_t s_xq[FD_MAX_T * FD_MAX_E];
+    __shared__ float s_xd[FD_MAX_T * FD_MAX_E / 32];
+    __shared__ __align__(16) int s_xbs[Q8K ? FD_MAX_T * FD_MAX_E / 16 : 4];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, gl = lane & (L_IN - 1), grp = lane / L_IN;
+    const int T = a.T, FE = a.FE, NU = a.NU, NE = a.NE, nbf = FE / 32, nu_in = fmt_units(TYPE, a.E);
+    stamp(a, 2);
+    for (int i = tid; i < (NE + 31) / 32; i += 512) bits[i] = 0u;
+    const float* lg = a.logits_in ? a.logits_in : a.logits;
+    if (w < T) {
+        router_select_one_wave(lg + (size_t)w * NE, NE, NU, s_ids[w], s_wts[w]);
+    } else {  // the other waves stage x meanwhile
+        const int i0 = tid - 64 * T, n = 512 - 64 * T, TE = T * a.E;
+        const int8_t* gq = Q8K ? a.xo.qK : a.xq;
+        const float* gd = Q8K ? a.xo.dK : a.xd;
+        for (int i = i0; i < TE / 16; i += n) ((uint4*)s_xq)[i] = ((const uint4*)gq)[i];
+        for (int i = i0; i < TE / (Q8K ? 256 : 32); i += n) s_xd[i] = gd[i];
+        if constexpr (Q8K)
+            for (int i = i0; i < TE / 64; i += n) ((int4*)s_xbs)[i] = ((const int4*)a.xo.bsK)[i];
+    }
+    __syncthreads();
+    if (tid < T * NU) {
+        const int t = tid / NU, j = tid - t * NU;
+        const int e = s_ids[t][j];
+        atomicOr(&bits[e >> 5], 1u << (e & 31));
+        if (blockIdx.x == 0) {  // the routing for kernel 3 and the caller
+            a.ids[tid] = e;
+            a.wts[tid] = s_wts[t][j];
+            if (a.ids_out) a.ids_out[tid] = e;
+            if (a.wts_out) a.wts_out[tid] = s_wts[t][j];
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {  // the union: routed experts ascending, then the shared one
+        int n = 0;
+        for (int wd = 0; wd < (NE + 31) / 32; ++wd)
+            for (uint32_t m = bits[wd]; m; m &= m - 1) ulist[n++] = 32 * wd + __ffs(m) - 1;
+        if (a.NS > NU) ulist[n++] = -1;
+        s_nu = n;
+    }
+    __syncthreads();
+    stamp(a, 3);
+    const int u = blockIdx.x / nbf, b = blockIdx.x - u * nbf;
+    if (u >= s_nu) return;  // (uniform) past the union's end
+    const int e = ulist[u];
+    const int mat = w / WPM, r0 = RW * (w % WPM) + grp * R;  // gate or up; this group's first row of the unit's 32
+    {
+        const int mi = e >= 0 ? mat : 3 + mat;
+        const long long rbase = (e >= 0 ? (long long)e * FE : 0) + 32 * b + r0;
+        const uint8_t* vb = pick(a.v, mi) + rbase * a.vrb_in;
+        const uint8_t* sb = pick(a.s, mi) + rbase * a.srb_in;
+        WUnit<TYPE> wu[NUPL_IN][R];
+#pragma unroll
+        for (int i = 0; i < NUPL_IN; ++i)
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                load_unit<TYPE, true>(vb + (long long)r * a.vrb_in, sb + (long long)r * a.srb_in, gl + i * L_IN,
+                                      nu_in, wu[i][r]);
+        if (tid < T) s_slot[tid] = slot_of(s_ids[tid], NU, e);
+        __syncthreads();
+        for (int t = 0; t < T; ++t) {
+            if (s_slot[t] < 0) continue;  // (uniform)
+            XUnit<TYPE> x[NUPL_IN];
+#pragma unroll
+            for (int i = 0; i < NUPL_IN; ++i) {
+                if constexpr (Q8K)
+                    load_x<TYPE>(s_xq + t * a.E, s_xd + t * (a.E / 256), s_xbs + t * (a.E / 16), gl + i * L_IN, x[i]);
+                else
+                    load_x<TYPE>(s_xq + t * a.E, s_xd + t * (a.E / 32), nullptr, gl + i * L_IN, x[i]);
+            }
+            float acc[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                acc[r] = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NUPL_IN; ++i) acc[r] += term<TYPE>(wu[i][r], x[i], gl + i * L_IN);
+                acc[r] = group_sum<L_IN>(acc[r]);
+            }
+            if (gl == 0) {
+                if constexpr (Q8K) {  // row (token t, its slot of e) of the fp32 gate / up
+                    float* o = (mat ? a.u : a.g) + ((long long)t * a.NS + s_slot[t]) * FE + 32 * b + r0;
+#pragma unroll
+                    for (int r = 0; r < R; ++r) o[r] = acc[r];
+                } else {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) gu[mat][t][r0 + r] = acc[r];
+                }
+            }
+        }
+    }
+    stamp(a, 7);
+    if constexpr (!Q8K) {
+        __syncthreads();
+        if (w < T && s_slot[w] >= 0) {  // token w's SwiGLU and Q8_0 block for its slot of e
+            const long long sl = (long long)w * a.NS + s_slot[w];
+            swiglu_q8_block(gu[0][w], gu[1][w], a.act_q + sl * FE + 32 * b, a.act_d + sl * nbf + b);
+        }
+    }
+    stamp(a, 4);
+}
+
 // ---- kernel 3: down rows i0 .. i0 + RB - 1 for every (token, slot) pair -- the items, a flat list, taken by the
 // waves IB at a time with all their loads issued together -- then the combine per token in slot order (the
 // combine kernel's expression)
@@ -302,12 +423,29 @@ hipError_t launch_multi(const FArgs& a, const qmatvec_q8* qa, int kernels, hipSt
     hipError_t e = hipSuccess;
     const int nq = Fmt<TYPE>::Q8K ? a.T * (a.E / 256) : a.T;  // quantizing workgroups of kernel 1
     if (kernels & 1) e = launch_kernel(k_fm_logits, dim3(a.NE + nq + a.T * a.has_gate), dim3(256), 0, st, a);
-    if (e == hipSuccess && (kernels & 2))
-        e = launch_kernel(k_fm_gate_up<TYPE, LI, NI>, dim3(pairs < cus ? pairs : cus), dim3(1024), 0, st, a);
+    // gate / up: a workgroup per unit when the grid fits two 512-thread workgroups per CU (one round: each pays its
+    // own routing once), else the persistent form (routing once per CU, then rounds of units). Measured at
+    // config 1 (µs per layer, persistent / per unit): T = 2 28.7 / 26.8, T = 3 39.2 / 39.7, T = 7 67.7 / 76.5.
+    const int units = nsu * (a.FE / 32);
+    if (e == hipSuccess && (kernels & 2)) {
+        if (units <= 2 * cus)
+            e = launch_kernel(k_fm_gate_up_unit<TYPE, LI, NI>, dim3(units), dim3(512), 0, st, a);
+        else
+            e = launch_kernel(k_fm_gate_up<TYPE, LI, NI>, dim3(pairs < cus ? pairs : cus), dim3(1024), 0, st, a);
+    }
     if (Fmt<TYPE>::Q8K && e == hipSuccess && (kernels & 2))
         e = gpu_swiglu(a.g, a.u, a.act, a.T * a.NS * a.FE, qa, st);
-    if (e == hipSuccess && (kernels & 4))
-        e = launch_kernel(k_fm_down<TYPE, LO, NO>, dim3(a.E / (64 / LO)), dim3(1024), 0, st, a);
+    // down + combine: per token (the T = 1 kernel over T rows of workgroups, one wave per slot) for Q8_0 and up to
+    // T = 3; the item-list kernel for the 4-bit types from T = 4 (its 8-row workgroups share an expert's rows among
+    // the tokens that chose it: config 1 T = 4 43.6 against 44.4 µs, T = 7 65.5 against 67.7). Q8_0's units
+    // need more registers than the item-list kernel's batches have at 1,024 threads (config 0 T = 2: 29 against
+    // 43 µs).
+    if (e == hipSuccess && (kernels & 4)) {
+        if (TYPE == QT_Q8_0 || a.T <= 3)
+            e = moe_fused_launch_down(TYPE, a, st);
+        else
+            e = launch_kernel(k_fm_down<TYPE, LO, NO>, dim3(a.E / (64 / LO)), dim3(1024), 0, st, a);
+    }
     return e;
 }
 
