@@ -144,11 +144,12 @@ __global__ void __launch_bounds__(64 * GROUP_WAVES) k_moe_group(const int* ids, 
 // waves, one token per lane).
 //   k_group_count: per block, the 64-bit expert masks of its 4 waves, then per expert the block's entry count
 //                  into ws[block][expert];
-//   k_group_scan:  one workgroup: per expert the exclusive scan over the blocks (ws becomes each block's offset
-//                  within the expert's run) and the total, then the scans over the experts and the tile table
-//                  (k_moe_group's code) and the experts' first entries into eoff;
-//   k_group_place: per block, the masks again, the wave prefixes, and each entry's position: eoff + the block's
-//                  offset + the wave prefix + the popcount of its wave's mask below its lane.
+//   k_group_place: per block, from the counts: each expert's total and this block's offset within the expert's
+//                  run (the blocks before it), the exclusive scan over the experts (their first entries; block
+//                  0 also scans the tile counts and writes the tile table, k_moe_group's rules); then the masks
+//                  again, the wave prefixes, and each entry's position: the expert's first entry + the block's
+//                  offset + the wave prefix + the popcount of its wave's mask below its lane. (Every block redoes
+//                  the scans over at most 1,024 experts: cheaper than a launch between the two kernels.)
 #define GB_WAVES 4
 
 __device__ __forceinline__ void block_masks(const int* ids, int T, int nu, int ne, unsigned long long* masks, int t,
@@ -176,59 +177,78 @@ __global__ void __launch_bounds__(64 * GB_WAVES) k_group_count(const int* ids, i
     }
 }
 
-__global__ void __launch_bounds__(1024) k_group_scan(int* ws, int nblk, int ne, int tile, int* eoff_out, int* n_tiles,
-                                                     int* tile_e, int* tile_start, int* tile_n) {
-    __shared__ int cnt[1024];
-    __shared__ int wpart[2][16];
+// Exclusive scan of v[0..n) in place by the 256-thread workgroup (4 consecutive values a thread), n <= 1024;
+// returns the total. part: 4 ints of LDS.
+__device__ int block256_exscan(int* v, int n, int* part) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    if (tid < ne) {  // the blocks' offsets within the expert's run, the expert's total
-        int off = 0;
-        for (int b = 0; b < nblk; ++b) {
-            const int c = ws[(size_t)b * ne + tid];
-            ws[(size_t)b * ne + tid] = off;
-            off += c;
-        }
-        cnt[tid] = off;
+    int x[4], s = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        x[k] = 4 * tid + k < n ? v[4 * tid + k] : 0;
+        s += x[k];
     }
-    __syncthreads();
-    const int c = tid < ne ? cnt[tid] : 0, nt = (c + tile - 1) / tile;
-    int a = c, bsum = nt;
+    int inc = s;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
-        const int ua = __shfl_up(a, d, 64), ub = __shfl_up(bsum, d, 64);
-        if (lane >= d) {
-            a += ua;
-            bsum += ub;
-        }
+        const int u = __shfl_up(inc, d, 64);
+        if (lane >= d) inc += u;
     }
-    if (lane == 63) {
-        wpart[0][w] = a;
-        wpart[1][w] = bsum;
-    }
+    if (lane == 63) part[w] = inc;
     __syncthreads();
-    int ba = 0, bb = 0;
-    for (int k = 0; k < w; ++k) {
-        ba += wpart[0][k];
-        bb += wpart[1][k];
-    }
-    const int eo = ba + a - c, to = bb + bsum - nt;
-    if (tid < ne) {
-        eoff_out[tid] = eo;
-        for (int k = 0; k < nt; ++k) {
-            tile_e[to + k] = tid;
-            tile_start[to + k] = eo + k * tile;
-            tile_n[to + k] = min(tile, c - k * tile);
+    int run = inc - s;
+    for (int k = 0; k < w; ++k) run += part[k];
+    const int total = (part[0] + part[1]) + (part[2] + part[3]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (4 * tid + k < n) {
+            v[4 * tid + k] = run;
+            run += x[k];
         }
-        if (tid == ne - 1) *n_tiles = to + nt;
-    }
+    __syncthreads();
+    return total;
 }
 
-__global__ void __launch_bounds__(64 * GB_WAVES) k_group_place(const int* ids, int T, int nu, int ne, const int* ws,
-                                                               const int* eoff, int* tok_rows, int* pair_rows) {
+__global__ void __launch_bounds__(64 * GB_WAVES) k_group_place(const int* ids, int T, int nu, int ne, int tile,
+                                                               const int* ws, int nblk, int* tok_rows, int* pair_rows,
+                                                               int* n_tiles, int* tile_e, int* tile_start,
+                                                               int* tile_n) {
     extern __shared__ unsigned long long g_smem[];
     unsigned long long* masks = g_smem;
     uint16_t* pre = (uint16_t*)(masks + (size_t)GB_WAVES * ne);  // [GB_WAVES][ne]
+    int* eoff = (int*)(pre + (size_t)GB_WAVES * ne);              // [ne] the experts' first entries
+    int* boff = eoff + ne;                                        // [ne] this block's offset in each run
+    int* tot = boff + ne;                                         // [ne] block 0: the experts' totals
+    int* tsc = tot + ne;                                          // [ne] block 0: tile counts, then first tiles
+    __shared__ int part[4];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, t = blockIdx.x * 64 * GB_WAVES + tid;
+    for (int e = tid; e < ne; e += 64 * GB_WAVES) {
+        int off = 0, all = 0;
+        for (int b = 0; b < nblk; ++b) {
+            const int c = ws[(size_t)b * ne + e];
+            off += b < (int)blockIdx.x ? c : 0;
+            all += c;
+        }
+        boff[e] = off;
+        eoff[e] = all;
+        if (blockIdx.x == 0) {
+            tot[e] = all;
+            tsc[e] = (all + tile - 1) / tile;
+        }
+    }
+    __syncthreads();
+    block256_exscan(eoff, ne, part);
+    if (blockIdx.x == 0) {  // the tile table (uniform branch)
+        const int nt = block256_exscan(tsc, ne, part);
+        for (int e = tid; e < ne; e += 64 * GB_WAVES) {
+            const int c = tot[e], k0 = tsc[e];
+            for (int k = 0; k * tile < c; ++k) {
+                tile_e[k0 + k] = e;
+                tile_start[k0 + k] = eoff[e] + k * tile;
+                tile_n[k0 + k] = min(tile, c - k * tile);
+            }
+        }
+        if (tid == 0) *n_tiles = nt;
+    }
     uint64_t vm;
     block_masks(ids, T, nu, ne, masks, t, vm);
     for (int e = tid; e < ne; e += 64 * GB_WAVES) {
@@ -241,7 +261,6 @@ __global__ void __launch_bounds__(64 * GB_WAVES) k_group_place(const int* ids, i
     }
     __syncthreads();
     const int* row = ids + (size_t)t * nu;
-    const int* boff = ws + (size_t)blockIdx.x * ne;
     const unsigned long long below = (1ull << lane) - 1ull;
     for (int j = 0; j < nu; ++j) {
         if (!((vm >> j) & 1)) continue;
@@ -255,7 +274,7 @@ __global__ void __launch_bounds__(64 * GB_WAVES) k_group_place(const int* ids, i
 extern "C" size_t gpu_moe_group_ws_bytes(int T, int n_expert) {
     if (T <= 0 || n_expert <= 0) return 0;
     const size_t nblk = ((size_t)T + 64 * GB_WAVES - 1) / (64 * GB_WAVES);
-    return (nblk + 1) * (size_t)n_expert * 4;
+    return nblk * (size_t)n_expert * 4;
 }
 
 extern "C" hipError_t gpu_moe_group_ws(const int* ids, int T, int n_used, int n_expert, int tile, int* tok_rows,
@@ -268,16 +287,13 @@ extern "C" hipError_t gpu_moe_group_ws(const int* ids, int T, int n_used, int n_
         return hipErrorInvalidValue;
     const int nblk = (T + 64 * GB_WAVES - 1) / (64 * GB_WAVES);
     int* cnt = (int*)ws;
-    int* eoff = cnt + (size_t)nblk * n_expert;
-    const size_t shm_c = (size_t)GB_WAVES * n_expert * 8, shm_p = shm_c + (size_t)GB_WAVES * n_expert * 2;
+    const size_t shm_c = (size_t)GB_WAVES * n_expert * 8,
+                 shm_p = shm_c + (size_t)GB_WAVES * n_expert * 2 + 4 * (size_t)n_expert * 4;
     hipError_t e = launch_kernel(k_group_count, dim3(nblk), dim3(64 * GB_WAVES), shm_c, stream, ids, T, n_used,
                                  n_expert, cnt);
     if (e == hipSuccess)
-        e = launch_kernel(k_group_scan, dim3(1), dim3(1024), 0, stream, cnt, nblk, n_expert, tile, eoff, n_tiles,
-                          tile_e, tile_start, tile_n);
-    if (e == hipSuccess)
         e = launch_kernel(k_group_place, dim3(nblk), dim3(64 * GB_WAVES), shm_p, stream, ids, T, n_used, n_expert,
-                          (const int*)cnt, (const int*)eoff, tok_rows, pair_rows);
+                          tile, (const int*)cnt, nblk, tok_rows, pair_rows, n_tiles, tile_e, tile_start, tile_n);
     return e;
 }
 
