@@ -189,15 +189,15 @@ __device__ __forceinline__ void q_issue(GBuf<QT_Q8_0, NM, KB>& B, int b0, uint4 
     }
 }
 
-template <int NM, int KB>
+template <int NM, int KB, int NTU>
 __device__ __forceinline__ void q_compute(const GBuf<QT_Q8_0, NM, KB>& B, const uint4 (&wsc)[NM],
-                                          v16f (&acc)[NM][GG_NT], int w, int l, int lr, int kh) {
+                                          v16f (&acc)[NM][NTU], int w, int l, int lr, int kh) {
     const v16i zi = {};
 #pragma unroll
     for (int bb = 0; bb < KB; ++bb) {
-        float dx[GG_NT];
+        float dx[NTU];
 #pragma unroll
-        for (int t = 0; t < GG_NT; ++t) dx[t] = B.dx[bb >> 2][32 * t + lr][bb & 3];
+        for (int t = 0; t < NTU; ++t) dx[t] = B.dx[bb >> 2][32 * t + lr][bb & 3];
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
             const uint32_t w2 = bb < 2 ? wsc[m].x : bb < 4 ? wsc[m].y : bb < 6 ? wsc[m].z : wsc[m].w;
@@ -205,7 +205,7 @@ __device__ __forceinline__ void q_compute(const GBuf<QT_Q8_0, NM, KB>& B, const 
             const v4i A = (v4i){(int)q.x, (int)q.y, (int)q.z, (int)q.w};
             const float dw = h2f((uint16_t)(w2 >> (16 * (bb & 1))));
 #pragma unroll
-            for (int t = 0; t < GG_NT; ++t) {
+            for (int t = 0; t < NTU; ++t) {
                 const v4i Bt = *(const v4i*)(B.b[bb][t] + 16 * l);
                 acc_block(acc[m][t], __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bt, zi, 0, 0, 0),
                           scale_outer(dw, dx[t], kh));
@@ -281,9 +281,9 @@ __device__ __forceinline__ void h_stage_b(HBuf<NM, KB>& B, const uint4 (&xb)[KB 
     }
 }
 
-template <int NM, int KB>
+template <int NM, int KB, int NTU>
 __device__ __forceinline__ void h_compute(const HBuf<NM, KB>& B, const uint4 (&wsc)[NM][KB / 4],
-                                          v16f (&acc)[NM][GG_NT], int w, int l, int lr) {
+                                          v16f (&acc)[NM][NTU], int w, int l, int lr) {
     const v16f z = {};
 #pragma unroll
     for (int bp = 0; bp < KB; bp += 2) {  // a block pair: 32 FP6 codes a lane, one conversion
@@ -301,7 +301,7 @@ __device__ __forceinline__ void h_compute(const HBuf<NM, KB>& B, const uint4 (&w
                 const v8h A0 = scaled8(d, 2 * k, __builtin_amdgcn_perm(sc, sc, 0x01000100u));      // (e0, e0)
                 const v8h A1 = scaled8(d, 2 * k + 1, __builtin_amdgcn_perm(sc, sc, 0x03020302u));  // (e1, e1)
 #pragma unroll
-                for (int t = 0; t < GG_NT; ++t) {
+                for (int t = 0; t < NTU; ++t) {
                     const float dx = B.dx[bb >> 2][32 * t + lr][bb & 3];
                     const v8h B0 = *(const v8h*)(B.b[bb][t][0] + 16 * l);
                     const v8h B1 = *(const v8h*)(B.b[bb][t][1] + 16 * l);
@@ -318,6 +318,10 @@ __device__ __forceinline__ void h_compute(const HBuf<NM, KB>& B, const uint4 (&w
 
 // ------------------------------------------------------------------ the kernel
 
+template <int TYPE, int NM, int KB, int NTU>
+__device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE, NM, KB>::type& buf, int k, int e,
+                                             int st, int cnt, bool shk);
+
 // NM = 1: y rows (fp32) of one matrix. NM = 2, SwiGLU: gate (a.v) and up (a.v2) rows of the same block, then
 // act = SiLU(g) u (the swiglu kernel's expression) and its Q8_0 blocks -- a wave's 32 rows of one entry are one
 // block: 16 values in each of lanes l and l + 32 -- into a.aq / a.ad (the quantizer's expressions).
@@ -331,7 +335,6 @@ __attribute__((amdgpu_waves_per_eu(GG_WPE)))
 #endif
 k_grouped(GArgs a) {
     __shared__ __attribute__((aligned(1024))) typename BufOf<TYPE, NM, KB>::type buf;
-    constexpr bool F16 = TYPE != QT_Q8_0;
     const int k = blockIdx.y;
     const bool shk = a.vs && k >= a.kr;  // a shared-expert tile
     int e, st, cnt;
@@ -351,6 +354,18 @@ k_grouped(GArgs a) {
         e = 0;
         cnt = min(GG_TILE, a.T - st);
     }
+    // a tile of at most 32 entries leaves its second 32-entry MFMA tile empty: the loop without it
+    if (cnt > 32)
+        grouped_tile<TYPE, NM, KB, GG_NT>(a, buf, k, e, st, cnt, shk);
+    else
+        grouped_tile<TYPE, NM, KB, 1>(a, buf, k, e, st, cnt, shk);
+}
+
+// One workgroup's tile k (expert e, entries st .. st + cnt - 1) with NTU of its GG_NT 32-entry MFMA tiles in use
+template <int TYPE, int NM, int KB, int NTU>
+__device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE, NM, KB>::type& buf, int k, int e,
+                                             int st, int cnt, bool shk) {
+    constexpr bool F16 = TYPE != QT_Q8_0;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lr = l & 31, kh = l >> 5;
     auto in_row = [&](int i) { return !shk && a.in_rows ? a.in_rows[st + i] : st + i; };
     auto out_row = [&](int i) { return shk ? a.sout + st + i : a.out_rows ? a.out_rows[st + i] : st + i; };
@@ -372,11 +387,11 @@ k_grouped(GArgs a) {
     const int de = min(GG_TILE / 4 * w + (l & (GG_TILE / 4 - 1)), cnt - 1);  // the entry whose scales this lane loads
     const float* dxr = a.xd + ((a.xt & GX_IN) ? (long long)k * GG_TILE + de : (long long)in_row(de)) * nb;
 
-    v16f acc[NM][GG_NT];
+    v16f acc[NM][NTU];
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int t = 0; t < GG_NT; ++t) acc[m][t] = (v16f){};
+        for (int t = 0; t < NTU; ++t) acc[m][t] = (v16f){};
     const int nst = nb / KB;
     if constexpr (!F16) {
         // this lane's activation run: entry 32 (w % GG_NT) + lr, K half kh
@@ -394,7 +409,7 @@ k_grouped(GArgs a) {
             q_issue<NM, KB>(buf, s * KB, wsc, vt, sct, xrow, xs, dxr, w, l);
             wait_vm<0>();
             __syncthreads();
-            q_compute<NM, KB>(buf, wsc, acc, w, l, lr, kh);
+            q_compute<NM, KB, NTU>(buf, wsc, acc, w, l, lr, kh);
             __syncthreads();
         }
     } else {
@@ -416,14 +431,14 @@ k_grouped(GArgs a) {
             wait_vm<0>();
             h_stage_b<NM, KB>(buf, xb, tid);
             __syncthreads();
-            h_compute<NM, KB>(buf, wsc, acc, w, l, lr);
+            h_compute<NM, KB, NTU>(buf, wsc, acc, w, l, lr);
             __syncthreads();
         }
     }
     // acc[m][t][j] is C[row 8 (j / 4) + 4 kh + j % 4][entry 32 t + lr] of the wave's 32 x GG_TILE block
     if constexpr (NM == 1) {
 #pragma unroll
-        for (int t = 0; t < GG_NT; ++t)
+        for (int t = 0; t < NTU; ++t)
             if (32 * t + lr < cnt) {
                 float* y = a.y + (long long)out_row(32 * t + lr) * a.ldy + r0;
 #pragma unroll
@@ -431,7 +446,7 @@ k_grouped(GArgs a) {
             }
     } else {
 #pragma unroll
-        for (int t = 0; t < GG_NT; ++t) {
+        for (int t = 0; t < NTU; ++t) {
             float act[16];
             float am = 0.0f;
 #pragma unroll
