@@ -211,35 +211,62 @@ __global__ void __launch_bounds__(256) k_matmul_f32(const float* W, long long ld
 
 // Prefill on fp32 MFMA (v_mfma_f32_32x32x2f32, exact fp32 products): one 32-token x 32-row output tile per
 // workgroup, its MF_KS waves each 1 / MF_KS of K (more waves in flight to cover the loads' latency), summed through
-// LDS in a fixed order. Both operands are rows along K, so lane l reads 16 consecutive values (64 bytes) of token /
-// weight row l % 32 per 32-value chunk (its half l / 32 of the chunk), and MFMA q of the chunk pairs value q of both
-// lanes' runs: k = chunk + 16 h + q on both sides. The next chunk's loads are issued before the current chunk's 16
-// MFMAs. K % (32 MF_KS) == 0.
+// LDS in a fixed order. Both operands are rows along K; lane l holds 16 consecutive values (64 bytes) of token /
+// weight row l % 32 per 32-value chunk (its half l / 32 of the chunk), and MFMA q of the chunk pairs value q of
+// both lanes' runs: k = chunk + 16 h + q on both sides. K % (32 MF_KS) == 0.
+// Each wave stages its chunks through its own 8 KB of LDS with LDS-direct loads (eight lanes per 128-byte row
+// segment: 8 cache lines per load instead of the 32 of loads in MFMA layout), the 16-byte pieces of row r stored
+// XOR-swizzled by (r / 2) % 8 so that the MFMA-layout reads of 16 lanes at a time hit 16 distinct bank groups.
+// Per chunk: its operands to registers, the next chunk's loads into the same LDS, then the 16 MFMAs.
 // Workgroups go to the 8 XCDs in turn (linear id L on XCD L % 8), so the grid is one-dimensional and L = 8 j + c
 // takes token tile 8 (j / nx) + c, row tile j % nx: the nx workgroups of a token tile share one XCD's L2, which
 // then fetches the tile's 32 token rows once (a row tile per grid column had spread them over all 8).
 typedef float mf_v16f __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void mf_lds_void;
 #ifndef MF_KS
 #define MF_KS 8
 #endif
 __global__ void __launch_bounds__(64 * MF_KS) k_matmul_f32_mfma(const float* W, long long ldw, const float* X,
                                                                float* Y, int N, int K, int T) {
-    __shared__ float red[MF_KS - 1][16][64];
-    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, h = l >> 5;
+    __shared__ __align__(16) float stage[MF_KS][2][32 * 32];  // [wave][tokens / rows][row * 32 + value]
+    static_assert((MF_KS - 1) * 16 * 64 <= MF_KS * 2 * 32 * 32, "the partial sums reuse the stage buffers");
+    float (*red)[16][64] = (float (*)[16][64])&stage[0][0][0];  // after the loop: waves 1.. partial sums
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, h = l >> 5, r = l & 31;
     const int nx = (N + 31) / 32, xc = blockIdx.x & 7, j = blockIdx.x >> 3;
     const int r0 = (j % nx) * 32, t0 = (8 * (j / nx) + xc) * 32;
     if (t0 >= T) return;  // (the last round of token tiles on some XCDs; uniform)
     const int kq = K / MF_KS, kb = w * kq;  // this wave's share of K
-    const float* xr = X + (size_t)min(t0 + (l & 31), T - 1) * K + kb + 16 * h;  // (rows past the end: the last
-    const float* wr = W + (size_t)min(r0 + (l & 31), N - 1) * ldw + kb + 16 * h;  //  row, results unused)
-    float4 xa[4], wa[4], xn[4], wn[4];
+    // load i of a chunk: lane l brings row 8 i + l / 8, piece (l % 8) ^ swz(row) of the row's 128 bytes
+    const float* gx[4];
+    const float* gw[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) xa[q] = ((const float4*)xr)[q], wa[q] = ((const float4*)wr)[q];
+    for (int i = 0; i < 4; ++i) {
+        const int row = 8 * i + (l >> 3), piece = (l & 7) ^ ((row >> 1) & 7);
+        gx[i] = X + (size_t)min(t0 + row, T - 1) * K + kb + 4 * piece;  // (rows past the end: the last row,
+        gw[i] = W + (size_t)min(r0 + row, N - 1) * ldw + kb + 4 * piece;  //  results unused)
+    }
+    float* sx = stage[w][0];
+    float* sw = stage[w][1];
+    auto issue = [&](int c) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_global_load_lds(gx[i] + c, (mf_lds_void*)(sx + 256 * i), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(gw[i] + c, (mf_lds_void*)(sw + 256 * i), 16, 0, 0);
+        }
+    };
+    issue(0);
     mf_v16f acc = {};
-    for (int c = 32; c <= kq; c += 32) {
-        if (c < kq)
+    for (int c = 0; c < kq; c += 32) {
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this chunk's pieces are in LDS
+        float4 xa[4], wa[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) xn[q] = ((const float4*)(xr + c))[q], wn[q] = ((const float4*)(wr + c))[q];
+        for (int q = 0; q < 4; ++q) {  // piece 4 h + q of row r, where the swizzle put it
+            const int at = 32 * r + 4 * ((4 * h + q) ^ ((r >> 1) & 7));
+            xa[q] = *(const float4*)(sx + at);
+            wa[q] = *(const float4*)(sw + at);
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the reads are done before the next loads overwrite
+        if (c + 32 < kq) issue(c + 32);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[q].x, wa[q].x, acc, 0, 0, 0);
@@ -247,9 +274,8 @@ __global__ void __launch_bounds__(64 * MF_KS) k_matmul_f32_mfma(const float* W, 
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[q].z, wa[q].z, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[q].w, wa[q].w, acc, 0, 0, 0);
         }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) xa[q] = xn[q], wa[q] = wn[q];
     }
+    __syncthreads();  // every wave is past its stage buffer
     if (w > 0)
 #pragma unroll
         for (int i = 0; i < 16; ++i) red[w - 1][i][l] = acc[i];
@@ -260,8 +286,8 @@ __global__ void __launch_bounds__(64 * MF_KS) k_matmul_f32_mfma(const float* W, 
             float v = acc[i];
 #pragma unroll
             for (int q = 0; q < MF_KS - 1; ++q) v += red[q][i][l];
-            const int t = t0 + 8 * (i >> 2) + 4 * h + (i & 3), r = r0 + (l & 31);
-            if (t < T && r < N) Y[(size_t)t * N + r] = v;
+            const int t = t0 + 8 * (i >> 2) + 4 * h + (i & 3), rr = r0 + (l & 31);
+            if (t < T && rr < N) Y[(size_t)t * N + rr] = v;
         }
     }
 }
