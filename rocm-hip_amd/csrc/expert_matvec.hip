@@ -536,6 +536,9 @@ extern "C" hipError_t qmatvec_launch_q8_id_x(int type, const void* W, const void
                                              size_t row_bytes, const int32_t* ids, int n_used, int x_per_slot,
                                              const qmatvec_q8* q, float* y, float* y2, int N, int K, int T,
                                              hipStream_t stream) {
+    // the reference's order (src/qmatvec.cpp:550-554): an unsupported type / K first, then shapes and capacity
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (!qmatvec_q8_supported(type, K)) return hipErrorInvalidDeviceFunction;
     if (T <= 0 || n_used <= 0 || N <= 0 || !ids || !y || (W2 && !y2)) return hipErrorInvalidValue;
     const hipError_t c = check_common(type, W, row_bytes, q, K, (long long)T * (x_per_slot ? n_used : 1));
     if (c != hipSuccess) return c;
@@ -666,11 +669,12 @@ extern "C" hipError_t qmatvec_launch_q8_id_batch(int type, const void* W, size_t
                                                  const int32_t* n_tiles, const int32_t* tile_e,
                                                  const int32_t* tile_start, const int32_t* tile_n,
                                                  const int32_t* in_rows, const int32_t* out_rows, hipStream_t stream) {
+    // the reference's order (src/qmatvec.cpp:601-604): an unsupported type / K first, then the rest
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (!qmatvec_q8_supported(type, K)) return hipErrorInvalidDeviceFunction;
     if (N <= 0 || max_tiles <= 0 || tile <= 0 || tile > qmatvec_id_batch_tile(type, N, K) || !y || !n_tiles ||
         !tile_e || !tile_start || !tile_n || !in_rows || !out_rows)
         return hipErrorInvalidValue;
-    if (!moe_lib_ready()) return hipErrorNotInitialized;
-    if (!qmatvec_q8_supported(type, K)) return hipErrorInvalidDeviceFunction;
     if (!W || !q || row_bytes != native_row(type, K) || !aligned(W, 4)) return hipErrorInvalidValue;
     const uint8_t *v = nullptr, *s = nullptr;
     long long vgs = 0, sgs = 0;
