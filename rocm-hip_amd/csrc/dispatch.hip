@@ -13,6 +13,8 @@
 // offset + the entries of earlier chunks + its wave's prefix + the popcount of its wave's mask below its lane.
 // A token's repeated id (a malformed row) and ids outside [0, n_expert) are skipped everywhere.
 
+#include <atomic>
+
 #include "gpu_ops.h"
 #include "host_common.h"
 #include "moe_common.h"
@@ -309,12 +311,12 @@ extern "C" hipError_t gpu_moe_group(const int* ids, int T, int n_used, int n_exp
         (long long)T * n_used > 0x7fffffffLL)
         return hipErrorInvalidValue;
     const size_t shm = group_smem(n_expert);
-    static bool attr_set = false;
-    if (!attr_set) {
+    static std::atomic<bool> attr_set{false};  // (setting it twice from racing threads is harmless)
+    if (!attr_set.load(std::memory_order_acquire)) {
         const hipError_t e = hipFuncSetAttribute((const void*)k_moe_group, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int)group_smem(1024));
         if (e != hipSuccess) return e;
-        attr_set = true;
+        attr_set.store(true, std::memory_order_release);
     }
     return launch_kernel(k_moe_group, dim3(1), dim3(64 * GROUP_WAVES), shm, stream, ids, T, n_used, n_expert, tile, tok_rows,
                          pair_rows, n_tiles, tile_e, tile_start, tile_n);

@@ -15,6 +15,8 @@
 // (A single persistent kernel with two grid barriers was measured slower: each barrier's cross-XCD fences and
 // 256-way atomic arrival cost ~10 us on MI355X, more than a kernel boundary.)
 
+#include <atomic>
+
 #include "fused_common.h"
 #include "gpu_ops.h"
 #include "host_common.h"
@@ -355,12 +357,14 @@ hipError_t moe_fused_launch_down(int type, const FArgs& a, hipStream_t st) {
     }
 }
 
-static unsigned long long* g_stamps = nullptr;
+static std::atomic<unsigned long long*> g_stamps{nullptr};
 
 // Profiling: every later fused layer writes timestamps to stamps (device memory of 8 words per workgroup of the
 // largest of the three grids; nullptr: stop)
-extern "C" void moe_layer_fused_stamps(void* stamps) { g_stamps = (unsigned long long*)stamps; }
-unsigned long long* moe_fused_stamps_ptr() { return g_stamps; }
+extern "C" void moe_layer_fused_stamps(void* stamps) {
+    g_stamps.store((unsigned long long*)stamps, std::memory_order_relaxed);
+}
+unsigned long long* moe_fused_stamps_ptr() { return g_stamps.load(std::memory_order_relaxed); }
 
 bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits, float* out, int* ids_out,
                    float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err, const FNorm* norm) {

@@ -17,6 +17,8 @@
 // Each row dot has the per-operation kernel's lane shape and order for its K, the router, quantizer, SwiGLU and
 // combine are the per-operation expressions, so the layer equals the per-operation path bit for bit.
 
+#include <atomic>
+
 #include "fused_common.h"
 #include "gpu_ops.h"
 #include "host_common.h"
@@ -466,8 +468,8 @@ hipError_t launch_multi_t(const FArgs& a, const qmatvec_q8* qa, int li, int ni, 
 
 }  // namespace
 
-static bool g_fm_q4k = false;  // Q4_K through the multi-token kernels (the parity tests turn it on)
-extern "C" void moe_layer_fused_multi_q4k(int on) { g_fm_q4k = on != 0; }
+static std::atomic<bool> g_fm_q4k{false};  // Q4_K through the multi-token kernels (the parity tests turn it on)
+extern "C" void moe_layer_fused_multi_q4k(int on) { g_fm_q4k.store(on != 0, std::memory_order_relaxed); }
 
 // T = 2..FD_MAX_T tokens through the multi-token kernels, when moe_fused_prepare takes the layer
 bool moe_fused_multi_try(const moe_layer_desc* d, const float* x, const float* logits, int T, float* out,
@@ -475,7 +477,7 @@ bool moe_fused_multi_try(const moe_layer_desc* d, const float* x, const float* l
     // Q4_K: the per-operation path. These kernels are bit-exact for it, but with 256 experts few rows are shared
     // between tokens and the per-operation id-batch launches read the rows faster (config-3 shape, T = 4: 55.5 us
     // against 71 us per layer).
-    if (T < 2 || T > FD_MAX_T || (d->type == QT_Q4_K && !g_fm_q4k)) return false;
+    if (T < 2 || T > FD_MAX_T || (d->type == QT_Q4_K && !g_fm_q4k.load(std::memory_order_relaxed))) return false;
     FArgs a = {};
     if (!moe_fused_prepare(d, a)) return false;
     if (a.NS > 17 || T * a.NU > 64) return false;  // (the union and the per-token slot tables' sizes)
