@@ -67,10 +67,20 @@ __device__ __forceinline__ float rms_first_pass(const float* xr, const float* ar
                                                 float* part) {
     const int t = threadIdx.x;
     float ss = 0.0f;
+    // every load unconditional (past the end: the last value, unused) so that all of them are in flight at once;
+    // a load under a per-value branch had each pair wait for the previous one
+    float xv[16];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        const int i = t + 256 * k;
-        keep[k] = i < n ? (ar ? xr[i] + ar[i] : xr[i]) : 0.0f;
+    for (int k = 0; k < 16; ++k) xv[k] = xr[min(t + 256 * k, n - 1)];
+    if (ar) {
+        float av[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) av[k] = ar[min(t + 256 * k, n - 1)];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) keep[k] = t + 256 * k < n ? xv[k] + av[k] : 0.0f;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) keep[k] = t + 256 * k < n ? xv[k] : 0.0f;
     }
 #pragma unroll
     for (int k = 0; k < 16; ++k) ss += keep[k] * keep[k];

@@ -37,6 +37,15 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
     const int tid = threadIdx.x, E = a.E;
     stamp(a, 0);
     const float* xv = a.x;
+    // router-row workgroups with the norm: the row's loads are issued first (they do not wait for the norm), then
+    // the dot takes f32_row_dot's order (16-byte loads, lane i, i + 256, ... of the row) and sums
+    const float* wrow = a.w_router + (size_t)blockIdx.x * E;
+    const bool pre = a.norm && (int)blockIdx.x < a.NE && (E & 3) == 0 && ((uintptr_t)wrow & 15) == 0;
+    float4 wpre[FD_MAX_E / 1024];
+    if (pre)
+#pragma unroll
+        for (int k = 0; k < FD_MAX_E / 1024; ++k)
+            if (tid + 256 * k < E / 4) wpre[k] = ((const float4*)wrow)[tid + 256 * k];
     if (a.norm) {  // every workgroup forms the normalized input itself (E <= 4096 values, from L2)
         float keep[16];
         const float inv = rms_first_pass(a.x, a.add, E, a.eps, keep, part);
@@ -53,7 +62,22 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
         xv = ys;
     }
     if ((int)blockIdx.x < a.NE) {
-        const float y = f32_row_dot(a.w_router + (size_t)blockIdx.x * E, xv, E, part);
+        float y;
+        if (pre) {  // (ys is 16-byte aligned LDS)
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < FD_MAX_E / 1024; ++k)
+                if (tid + 256 * k < E / 4) {
+                    const float4 w4 = wpre[k], b = ((const float4*)xv)[tid + 256 * k];
+                    acc = fmaf(w4.x, b.x, acc);
+                    acc = fmaf(w4.y, b.y, acc);
+                    acc = fmaf(w4.z, b.z, acc);
+                    acc = fmaf(w4.w, b.w, acc);
+                }
+            y = block256_sum(acc, part);
+        } else {
+            y = f32_row_dot(wrow, xv, E, part);
+        }
         if (tid == 0) a.logits[blockIdx.x] = y;
         stamp(a, 1);
         return;
