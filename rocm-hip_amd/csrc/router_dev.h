@@ -100,9 +100,11 @@ __device__ __forceinline__ void router_select_wave(const float* lg, int ne, int 
     uint32_t key[NPL];
     float mx = -INFINITY;
 #pragma unroll
+    for (int j = 0; j < NPL; ++j) v[j] = lg[min(lane + 64 * j, ne - 1)];  // (all loads in flight at once)
+#pragma unroll
     for (int j = 0; j < NPL; ++j) {
         const int e = lane + 64 * j;
-        v[j] = e < ne ? lg[e] : -INFINITY;
+        if (e >= ne) v[j] = -INFINITY;
         key[j] = e < ne ? f32_order_key(v[j] == 0.0f ? 0.0f : v[j]) : 0u;
         mx = fmaxf(mx, v[j]);
     }
