@@ -155,8 +155,8 @@ __global__ void __launch_bounds__(1024) k_fm_gate_up(FArgs a) {
         const int u = k / nbf, b = k - u * nbf, e = ulist[u];
         const int mi = e >= 0 ? mat : 3 + mat;
         const long long rbase = (e >= 0 ? (long long)e * FE : 0) + 32 * b + r0;
-        const uint8_t* vb = pick(a.v, mi) + rbase * a.vrb_in;
-        const uint8_t* sb = pick(a.s, mi) + rbase * a.srb_in;
+        const uint8_t* vb = pick_opaque(a.v, mi) + rbase * a.vrb_in;
+        const uint8_t* sb = pick_opaque(a.s, mi) + rbase * a.srb_in;
 #pragma unroll
         for (int i = 0; i < NUPL_IN; ++i)
 #pragma unroll
@@ -375,8 +375,8 @@ __global__ void __launch_bounds__(1024) k_fm_down(FArgs a) {
                 const int e = s_e[k];
                 const long long row = e >= 0 ? (long long)e * E + i0 + i : i0 + i;
                 const int mi = e >= 0 ? 2 : 5;
-                const uint8_t* vr = pick(a.v, mi) + row * a.vrb_out;
-                const uint8_t* sr = pick(a.s, mi) + row * a.srb_out;
+                const uint8_t* vr = pick_opaque(a.v, mi) + row * a.vrb_out;
+                const uint8_t* sr = pick_opaque(a.s, mi) + row * a.srb_out;
 #pragma unroll
                 for (int c = 0; c < NUPL_OUT; ++c) load_packed<TYPE>(vr, sr, gl + c * L_OUT, nu_out, wu[q][c]);
 #pragma unroll

@@ -43,6 +43,24 @@ __device__ __forceinline__ T pick(const T (&p)[N], int i) {
     return r;
 }
 
+// pick for pointers where the optimizer folds pick's selects back into such a load (it did where i depends on a
+// value read from LDS, in the multi-token kernels): every element first passes, unconditionally, through an
+// empty asm statement that keeps it in scalar registers. (Not the default: it costs the T = 1 kernels ~0.7 µs.)
+template <int N, typename T>
+__device__ __forceinline__ T* pick_opaque(T* const (&p)[N], int i) {
+    T* q[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        uint64_t v = (uint64_t)p[k];
+        asm("" : "+s"(v));
+        q[k] = (T*)v;
+    }
+    T* r = q[0];
+#pragma unroll
+    for (int k = 1; k < N; ++k) r = i == k ? q[k] : r;
+    return r;
+}
+
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
 // UE4M3 scale byte at half scale: (8 + m) 2^(e - 11), subnormals m 2^-10, 0x7f and above 0
