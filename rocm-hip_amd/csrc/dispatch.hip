@@ -22,13 +22,14 @@
 #define GROUP_WAVES 8
 #define GROUP_MAX_NU 16  // ids of a token held in registers; wider rows read them from memory
 
-// Bit j: entry j of the token's row is the first occurrence of a valid expert id
-__device__ __forceinline__ uint64_t group_valid_mask(const int* row, int nu, int ne) {
+// Bit j: entry j of the token's row is the first occurrence of a valid expert id. Rows of at most GROUP_MAX_NU ids
+// are loaded into r at once (unconditional loads: under a per-id branch each one had waited for the previous);
+// wider rows are read from memory.
+__device__ __forceinline__ uint64_t group_valid_mask(const int* row, int nu, int ne, int (&r)[GROUP_MAX_NU]) {
     uint64_t m = 0;
     if (nu <= GROUP_MAX_NU) {
-        int r[GROUP_MAX_NU];
 #pragma unroll
-        for (int j = 0; j < GROUP_MAX_NU; ++j) r[j] = j < nu ? row[j] : -1;
+        for (int j = 0; j < GROUP_MAX_NU; ++j) r[j] = row[min(j, nu - 1)];
 #pragma unroll
         for (int j = 0; j < GROUP_MAX_NU; ++j) {
             bool ok = j < nu && r[j] >= 0 && r[j] < ne;
@@ -45,6 +46,19 @@ __device__ __forceinline__ uint64_t group_valid_mask(const int* row, int nu, int
         }
     }
     return m;
+}
+
+// f(j, e) for every valid entry j (bit j of vm) of the row, e its expert id (from r when the row fits it)
+template <typename F>
+__device__ __forceinline__ void for_valid(const int* row, int nu, uint64_t vm, const int (&r)[GROUP_MAX_NU], F f) {
+    if (nu <= GROUP_MAX_NU) {
+#pragma unroll
+        for (int j = 0; j < GROUP_MAX_NU; ++j)
+            if ((vm >> j) & 1) f(j, r[j]);
+    } else {
+        for (int j = 0; j < nu; ++j)
+            if ((vm >> j) & 1) f(j, row[j]);
+    }
 }
 
 __global__ void __launch_bounds__(64 * GROUP_WAVES) k_moe_group(const int* ids, int T, int nu, int ne, int tile,
@@ -70,9 +84,9 @@ __global__ void __launch_bounds__(64 * GROUP_WAVES) k_moe_group(const int* ids, 
             __syncthreads();
             const int t = t0 + tid;
             const int* row = ids + (size_t)t * nu;
-            const uint64_t vm = t < T ? group_valid_mask(row, nu, ne) : 0ull;
-            for (int j = 0; j < nu; ++j)
-                if ((vm >> j) & 1) atomicOr(&my[row[j]], 1ull << lane);
+            int r[GROUP_MAX_NU];
+            const uint64_t vm = t < T ? group_valid_mask(row, nu, ne, r) : 0ull;
+            for_valid(row, nu, vm, r, [&](int, int e) { atomicOr(&my[e], 1ull << lane); });
             __syncthreads();
             for (int e = tid; e < ne; e += NT) {  // prefixes over the waves, the chunk's count
                 int s = 0;
@@ -85,13 +99,11 @@ __global__ void __launch_bounds__(64 * GROUP_WAVES) k_moe_group(const int* ids, 
             }
             __syncthreads();
             if (pass == 1) {
-                for (int j = 0; j < nu; ++j) {
-                    if (!((vm >> j) & 1)) continue;
-                    const int e = row[j];
+                for_valid(row, nu, vm, r, [&](int j, int e) {
                     const int p = eoff[e] + run[e] + pre[(size_t)w * ne + e] + __popcll(my[e] & below);
                     tok_rows[p] = t;
                     pair_rows[p] = t * nu + j;
-                }
+                });
                 __syncthreads();
                 for (int e = tid; e < ne; e += NT)
                     run[e] += pre[(size_t)(GROUP_WAVES - 1) * ne + e] + __popcll(masks[(size_t)(GROUP_WAVES - 1) * ne + e]);
@@ -155,22 +167,22 @@ __global__ void __launch_bounds__(64 * GROUP_WAVES) k_moe_group(const int* ids, 
 #define GB_WAVES 4
 
 __device__ __forceinline__ void block_masks(const int* ids, int T, int nu, int ne, unsigned long long* masks, int t,
-                                            uint64_t& vm) {
+                                            uint64_t& vm, int (&r)[GROUP_MAX_NU]) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     unsigned long long* my = masks + (size_t)w * ne;
     for (int e = lane; e < ne; e += 64) my[e] = 0ull;
     __syncthreads();
     const int* row = ids + (size_t)t * nu;
-    vm = t < T ? group_valid_mask(row, nu, ne) : 0ull;
-    for (int j = 0; j < nu; ++j)
-        if ((vm >> j) & 1) atomicOr(&my[row[j]], 1ull << lane);
+    vm = t < T ? group_valid_mask(row, nu, ne, r) : 0ull;
+    for_valid(row, nu, vm, r, [&](int, int e) { atomicOr(&my[e], 1ull << lane); });
     __syncthreads();
 }
 
 __global__ void __launch_bounds__(64 * GB_WAVES) k_group_count(const int* ids, int T, int nu, int ne, int* ws) {
     extern __shared__ unsigned long long g_smem[];
     uint64_t vm;
-    block_masks(ids, T, nu, ne, g_smem, blockIdx.x * 64 * GB_WAVES + threadIdx.x, vm);
+    int r[GROUP_MAX_NU];
+    block_masks(ids, T, nu, ne, g_smem, blockIdx.x * 64 * GB_WAVES + threadIdx.x, vm, r);
     for (int e = threadIdx.x; e < ne; e += 64 * GB_WAVES) {
         int s = 0;
 #pragma unroll
@@ -252,7 +264,8 @@ __global__ void __launch_bounds__(64 * GB_WAVES) k_group_place(const int* ids, i
         if (tid == 0) *n_tiles = nt;
     }
     uint64_t vm;
-    block_masks(ids, T, nu, ne, masks, t, vm);
+    int r[GROUP_MAX_NU];
+    block_masks(ids, T, nu, ne, masks, t, vm, r);
     for (int e = tid; e < ne; e += 64 * GB_WAVES) {
         int s = 0;
 #pragma unroll
@@ -264,13 +277,11 @@ __global__ void __launch_bounds__(64 * GB_WAVES) k_group_place(const int* ids, i
     __syncthreads();
     const int* row = ids + (size_t)t * nu;
     const unsigned long long below = (1ull << lane) - 1ull;
-    for (int j = 0; j < nu; ++j) {
-        if (!((vm >> j) & 1)) continue;
-        const int e = row[j];
+    for_valid(row, nu, vm, r, [&](int j, int e) {
         const int p = eoff[e] + boff[e] + pre[(size_t)w * ne + e] + __popcll(masks[(size_t)w * ne + e] & below);
         tok_rows[p] = t;
         pair_rows[p] = t * nu + j;
-    }
+    });
 }
 
 extern "C" size_t gpu_moe_group_ws_bytes(int T, int n_expert) {
