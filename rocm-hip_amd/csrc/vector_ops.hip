@@ -91,7 +91,28 @@ __global__ void __launch_bounds__(256) k_combine(const float* down, const float*
     const float* w = wts ? wts + (size_t)t * nu : nullptr;
     auto ld = [&](const float* p) { return *(const vec*)p; };
     vec acc;
-    if (!wts) {  // weight 1 per expert
+    if (nu <= 16) {  // every slot's row loaded at once (a load per loop trip waited for the previous one)
+        vec v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = ld(d + (size_t)min(j, nu - 1) * n);
+        if (!wts) {
+            acc = v[0];
+#pragma unroll
+            for (int j = 1; j < 16; ++j)
+                if (j < nu) acc += v[j];
+        } else if (exp_scale) {
+            const int* e = ids + (size_t)t * nu;
+            acc = (v[0] * exp_scale[e[0]]) * w[0];
+#pragma unroll
+            for (int j = 1; j < 16; ++j)
+                if (j < nu) acc += (v[j] * exp_scale[e[j]]) * w[j];
+        } else {
+            acc = w[0] * v[0];
+#pragma unroll
+            for (int j = 1; j < 16; ++j)
+                if (j < nu) acc += w[j] * v[j];
+        }
+    } else if (!wts) {  // weight 1 per expert
         acc = ld(d);
         for (int j = 1; j < nu; ++j) acc += ld(d + (size_t)j * n);
     } else if (exp_scale) {
