@@ -47,6 +47,9 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
         for (int k = 0; k < FD_MAX_E / 1024; ++k)
             if (tid + 256 * k < E / 4) wpre[k] = ((const float4*)wrow)[tid + 256 * k];
     if (a.norm) {  // every workgroup forms the normalized input itself (E <= 4096 values, from L2)
+        float wn[16];  // the norm weights, loaded with x and add (under a per-value branch they had waited in turn)
+#pragma unroll
+        for (int k = 0; k < 16; ++k) wn[k] = a.w_norm ? a.w_norm[min(tid + 256 * k, E - 1)] : 1.0f;
         float keep[16];
         const float inv = rms_first_pass(a.x, a.add, E, a.eps, keep, part);
         const bool res = blockIdx.x == 0 && a.add && a.x_out;  // workgroup 0 writes the residual
@@ -54,7 +57,7 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
         for (int k = 0; k < 16; ++k) {
             const int i = tid + 256 * k;
             if (i < E) {
-                ys[i] = keep[k] * inv * (a.w_norm ? a.w_norm[i] : 1.0f);
+                ys[i] = keep[k] * inv * wn[k];
                 if (res) a.x_out[i] = keep[k];
             }
         }

@@ -142,7 +142,10 @@ __global__ void __launch_bounds__(256) k_add_rmsnorm(const float* x_in, const fl
     float keep[KEEP];
     const bool kept = n <= 256 * KEEP;
     float inv;
+    float wn[KEEP];  // kept rows: the weights, loaded with x and add
     if (kept) {
+#pragma unroll
+        for (int k = 0; k < KEEP; ++k) wn[k] = w ? w[min(t + 256 * k, n - 1)] : 1.0f;
         inv = rms_first_pass(xr, ar, n, eps, keep, part);
     } else {
         float ss = 0.0f;
@@ -157,13 +160,13 @@ __global__ void __launch_bounds__(256) k_add_rmsnorm(const float* x_in, const fl
         inv = 1.0f / sqrtf(tot / (float)n + eps);
     }
     const int nb = (n + 255) / 256;
-    auto block = [&](int b, float xv) {  // block b of 256 values: outputs, then the quantizer (uniform call)
+    auto block = [&](int b, float xv, float wv) {  // block b of 256 values: outputs, then the quantizer (uniform call)
         const int i = b * 256 + t;
         const bool act = i < n;
         float v = 0.0f;
         if (act) {
             if (ar) x_out[(size_t)row * n + i] = xv;
-            v = xv * inv * (w ? w[i] : 1.0f);
+            v = xv * inv * wv;
             y[(size_t)row * n + i] = v;
             half_copy(o, (long long)row * n + i, v);
         }
@@ -172,11 +175,11 @@ __global__ void __launch_bounds__(256) k_add_rmsnorm(const float* x_in, const fl
     if (kept) {
 #pragma unroll
         for (int b = 0; b < KEEP; ++b)
-            if (b < nb) block(b, keep[b]);
+            if (b < nb) block(b, keep[b], wn[b]);
     } else {
         for (int b = 0; b < nb; ++b) {
             const int i = b * 256 + t;
-            block(b, i < n ? (ar ? xr[i] + ar[i] : xr[i]) : 0.0f);
+            block(b, i < n ? (ar ? xr[i] + ar[i] : xr[i]) : 0.0f, w && i < n ? w[i] : 1.0f);
         }
     }
 }
