@@ -37,11 +37,20 @@ __global__ void __launch_bounds__(256) k_fm_logits(FArgs a) {
     const int b = blockIdx.x, tid = threadIdx.x, E = a.E, T = a.T;
     const int nq = a.xo.qK ? T * (E / 256) : T;
     stamp(a, 0);
-    if (b < a.NE) {  // the per-token F32 matvec's sums, one token after the other
-        for (int t = 0; t < T; ++t) {
-            const float y = f32_row_dot(a.w_router + (size_t)b * E, a.x + (size_t)t * E, E, part);
-            if (tid == 0) a.logits[(size_t)t * a.NE + b] = y;
-        }
+    if (b < a.NE) {  // the per-token F32 matvec's sums, every token in one pass over the router row
+        __shared__ float tpart[FD_MAX_T][4];
+        float y[FD_MAX_T];
+        const float* wr = a.w_router + (size_t)b * E;
+        if (T <= 2)  // (uniform: as many token registers as the batch needs)
+            f32_row_dot_multi<2>(wr, a.x, E, T, E, tpart, y);
+        else if (T <= 4)
+            f32_row_dot_multi<4>(wr, a.x, E, T, E, tpart, y);
+        else
+            f32_row_dot_multi<FD_MAX_T>(wr, a.x, E, T, E, tpart, y);
+        if (tid == 0)
+#pragma unroll
+            for (int t = 0; t < FD_MAX_T; ++t)
+                if (t < T) a.logits[(size_t)t * a.NE + b] = y[t];
     } else if (b < a.NE + nq) {
         if (a.xo.qK) {  // block blk of the [T][E] bundle: token blk / (E / 256)
             __shared__ Q8Smem sh;

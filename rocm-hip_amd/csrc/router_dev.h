@@ -38,6 +38,51 @@ __device__ __forceinline__ float f32_row_dot(const float* wr, const float* x, in
     return block256_sum(acc, part);
 }
 
+// W[row] . x[t] for tokens t < T (T <= TMAX; x rows ldx apart), the router row read once: per token the same fma
+// chain and workgroup sum as f32_row_dot, so the same bits. y[t] is valid in every thread.
+template <int TMAX>
+__device__ __forceinline__ void f32_row_dot_multi(const float* wr, const float* x, long long ldx, int T, int K,
+                                                  float (*part)[4], float y[TMAX]) {
+    const int tid = threadIdx.x;
+    float acc[TMAX];
+#pragma unroll
+    for (int t = 0; t < TMAX; ++t) acc[t] = 0.0f;
+    const bool vec = (K & 3) == 0 && (ldx & 3) == 0 && (((uintptr_t)wr | (uintptr_t)x) & 15) == 0;
+    if (vec) {
+        const float4* w4 = (const float4*)wr;
+        for (int i = tid; i < K / 4; i += 256) {
+            const float4 a = w4[i];
+            float4 b[TMAX];
+#pragma unroll
+            for (int t = 0; t < TMAX; ++t) b[t] = ((const float4*)(x + (size_t)min(t, T - 1) * ldx))[i];
+#pragma unroll
+            for (int t = 0; t < TMAX; ++t)
+                if (t < T) {
+                    acc[t] = fmaf(a.x, b[t].x, acc[t]);
+                    acc[t] = fmaf(a.y, b[t].y, acc[t]);
+                    acc[t] = fmaf(a.z, b[t].z, acc[t]);
+                    acc[t] = fmaf(a.w, b[t].w, acc[t]);
+                }
+        }
+    } else {
+        for (int i = tid; i < K; i += 256) {
+            const float a = wr[i];
+#pragma unroll
+            for (int t = 0; t < TMAX; ++t)
+                if (t < T) acc[t] = fmaf(a, x[(size_t)t * ldx + i], acc[t]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < TMAX; ++t) {
+        const float v = wave_sum(acc[t]);
+        if ((threadIdx.x & 63) == 0) part[t][threadIdx.x >> 6] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < TMAX; ++t) y[t] = (part[t][0] + part[t][1]) + (part[t][2] + part[t][3]);
+    __syncthreads();
+}
+
 // sigmoid(x . w) over n values (the shared expert's gate)
 __device__ __forceinline__ float shexp_gate(const float* xr, const float* w, int n, float* part) {
     const int tid = threadIdx.x;
