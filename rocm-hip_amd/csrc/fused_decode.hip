@@ -193,6 +193,104 @@ __global__ void __launch_bounds__(1024) k_fd_down(FArgs a) {
     stamp(a, 6);
 }
 
+// ---- kernel 3 for Q4_K (T = 1): down's Q8_K input formed here instead of by a SwiGLU launch between kernels 2 and
+// 3. Each slot's wave reads its slot's fp32 gate / up rows (FE = 1024: 16 consecutive values a lane, 16 lanes per
+// 256-value block), forms SiLU(g) u (the SwiGLU kernel's expression) and the Q8_K blocks (the quantizer's: the
+// signed value of largest |x| with the lowest index on ties, iscale = -127 / it, q = min(127, rint(iscale x)),
+// d = 1 / iscale, sums of 16), into its own LDS; its weight loads are issued first. Then RS sets of 64 / L_OUT
+// output rows with the per-operation down shape (L_OUT lanes, NUPL_OUT units a lane), and the combine in slot order.
+// The same bits as the SwiGLU kernel and kernel 3; RS row sets a workgroup keep the workgroups' redundant reads of
+// the gate / up rows at E / (RS 64 / L_OUT) x NS x 8 KB.
+#define FD_Q8K_FE 1024
+template <int L_OUT, int NUPL_OUT, int RS>
+__global__ void __launch_bounds__(1024) k_fd_down_q8k(FArgs a) {
+    constexpr int RB = 64 / L_OUT;
+    static_assert(L_OUT * NUPL_OUT * 64 == FD_Q8K_FE, "FE: one unit of 64 values a lane and unit");
+    __shared__ float downv[16][RB * RS];
+    __shared__ __align__(16) int8_t aq[16][FD_Q8K_FE];
+    __shared__ float adk[16][FD_Q8K_FE / 256];
+    __shared__ __align__(16) int abk[16][FD_Q8K_FE / 16];
+    const int tid = threadIdx.x, E = a.E, FE = a.FE, NU = a.NU, NS = a.NS;
+    const int slot = tid >> 6, lane = tid & 63, gl = lane & (L_OUT - 1), i = lane / L_OUT;
+    const int i0 = blockIdx.x * RB * RS;
+    stamp(a, 5);
+    const int e = slot < NU ? a.ids[slot] : -1;
+    const int mi = e >= 0 ? 2 : 5;
+    const long long rbase = e >= 0 ? (long long)e * E : 0;
+    const uint8_t* vb = pick(a.v, mi) + rbase * a.vrb_out;
+    const uint8_t* sb = pick(a.s, mi) + rbase * a.srb_out;
+    const int nu_out = fmt_units(QT_Q4_K, FE);
+    WUnit<QT_Q4_K> wu[RS][NUPL_OUT];
+#pragma unroll
+    for (int r = 0; r < RS; ++r) {
+        const long long row = i0 + RB * r + i;
+#pragma unroll
+        for (int c = 0; c < NUPL_OUT; ++c)
+            load_packed<QT_Q4_K>(vb + row * a.vrb_out, sb + row * a.srb_out, gl + c * L_OUT, nu_out, wu[r][c]);
+    }
+    {  // this slot's SwiGLU and Q8_K blocks
+        const float4* g4 = (const float4*)(a.g + (long long)slot * FE + 16 * lane);
+        const float4* u4 = (const float4*)(a.u + (long long)slot * FE + 16 * lane);
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 g = g4[k], u = u4[k];
+            const float gg[4] = {g.x, g.y, g.z, g.w}, uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[4 * k + j] = gg[j] / (1.0f + __expf(-gg[j])) * uu[j];
+        }
+        float ba = fabsf(v[0]), bv = v[0];
+        int bi = 16 * (lane & 15);  // index within the 256-value block
+#pragma unroll
+        for (int k = 1; k < 16; ++k)
+            if (fabsf(v[k]) > ba) {
+                ba = fabsf(v[k]);
+                bv = v[k];
+                bi = 16 * (lane & 15) + k;
+            }
+        argmax_step<1>(ba, bv, bi);
+        argmax_step<2>(ba, bv, bi);
+        argmax_step<4>(ba, bv, bi);
+        argmax_step<8>(ba, bv, bi);
+        const float iscale = ba != 0.0f ? -127.0f / bv : 0.0f;
+        int q[16], s16 = 0;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            q[k] = ba != 0.0f ? min(127, (int)rintf(iscale * v[k])) : 0;
+            s16 += q[k];
+        }
+        uint32_t pk[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            pk[k] = (q[4 * k] & 0xff) | ((q[4 * k + 1] & 0xff) << 8) | ((q[4 * k + 2] & 0xff) << 16) |
+                    ((uint32_t)q[4 * k + 3] << 24);
+        *(uint4*)&aq[slot][16 * lane] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        if ((lane & 15) == 0) adk[slot][lane >> 4] = ba != 0.0f ? 1.0f / iscale : 0.0f;
+        abk[slot][lane] = s16;
+    }
+    // (the slot's own wave reads what it wrote: LDS operations of a wave complete in order)
+    XUnit<QT_Q4_K> x[NUPL_OUT];
+#pragma unroll
+    for (int c = 0; c < NUPL_OUT; ++c) load_x<QT_Q4_K>(aq[slot], adk[slot], abk[slot], gl + c * L_OUT, x[c]);
+#pragma unroll
+    for (int r = 0; r < RS; ++r) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NUPL_OUT; ++c) acc += term<QT_Q4_K>(wu[r][c], x[c], gl + c * L_OUT);
+        acc = group_sum<L_OUT>(acc);
+        if (gl == 0) downv[slot][RB * r + i] = acc;
+    }
+    __syncthreads();
+    if (tid < RB * RS) {  // the combine kernel's expression
+        const float* wts = a.wts;
+        float o = wts[0] * downv[0][tid];
+        for (int j = 1; j < NU; ++j) o += wts[j] * downv[j][tid];
+        if (NS > NU) o += a.has_gate ? downv[NU][tid] * a.sg[0] : downv[NU][tid];
+        a.out[i0 + tid] = o;
+    }
+    stamp(a, 6);
+}
+
 // ------------------------------------------------------------------ host side
 
 bool moe_packed_planes(const void* W, int type, int K, size_t row_bytes, const uint8_t** v, const uint8_t** s);
@@ -208,8 +306,19 @@ hipError_t launch_fused(const FArgs& a, const qmatvec_q8* qa, int kernels, hipSt
     if (e == hipSuccess && (kernels & 2))
         e = launch_kernel(k_fd_gate_up<TYPE, LI, NI>, dim3(a.NS * (a.FE / 32)), dim3(64 * (64 / FD_GU_RW)), 0, st,
                           a);
-    if (Fmt<TYPE>::Q8K && e == hipSuccess && (kernels & 2))
-        e = gpu_swiglu(a.g, a.u, a.act, a.NS * a.FE, qa, st);
+#ifndef FD_Q8K_RS
+#define FD_Q8K_RS 4
+#endif
+    constexpr int RS = FD_Q8K_RS;  // Q4_K: row sets a kernel-3 workgroup
+    if constexpr (Fmt<TYPE>::Q8K) {  // down's Q8_K input formed by kernel 3 itself
+        if (e == hipSuccess && (kernels & 4)) {
+            if (a.FE == FD_Q8K_FE && a.E % (RS * (64 / LO)) == 0 && LO * NO * 64 == FD_Q8K_FE)
+                e = launch_kernel(k_fd_down_q8k<LO, NO, RS>, dim3(a.E / (RS * (64 / LO))), dim3(64 * a.NS), 0, st, a);
+            else if ((e = gpu_swiglu(a.g, a.u, a.act, a.NS * a.FE, qa, st)) == hipSuccess)
+                e = launch_kernel(k_fd_down<TYPE, LO, NO>, dim3(a.E / (64 / LO)), dim3(64 * a.NS), 0, st, a);
+        }
+        return e;
+    }
     if (e == hipSuccess && (kernels & 4))
         e = launch_kernel(k_fd_down<TYPE, LO, NO>, dim3(a.E / (64 / LO)), dim3(64 * a.NS), 0, st, a);
     return e;
