@@ -53,7 +53,7 @@ __device__ __forceinline__ T* pick_opaque(T* const (&p)[N], int i) {
     for (int k = 0; k < N; ++k) {
         uint64_t v = (uint64_t)p[k];
         asm("" : "+s"(v));
-        q[k] = (T*)v;
+        q[k] = (T*)(__attribute__((address_space(1))) T*)v;  // (a global pointer again: global, not flat, loads)
     }
     T* r = q[0];
 #pragma unroll
@@ -76,14 +76,14 @@ __device__ __forceinline__ float ue4m3_half(uint32_t e) {
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 // Four FP4 codes (the low nibble of each byte) -> four int8 codebook values {0,1,2,3,4,6,8,10} with bit 3 the
-// sign. v_perm_b32 picks byte (code & 7) of an 8-byte table of magnitudes and of one of negatives; a per-byte
-// mask built from bit 3 selects between them.
+// sign. v_perm_b32 picks byte (code & 7) of an 8-byte table of magnitudes and of one of negatives; a third
+// v_perm_b32 takes byte k of the magnitudes (selector k) or of the negatives (k + 4, bit 3 moved to bit 2).
+// (All full-rate: a byte mask made by multiplying the sign bits by 0xff was a quarter-rate v_mul_lo_u32.)
 __device__ __forceinline__ uint32_t fp4x4_to_i8x4(uint32_t n) {
     const uint32_t sel = n & 0x07070707u;
     const uint32_t pos = __builtin_amdgcn_perm(0x0a080604u, 0x03020100u, sel);
     const uint32_t neg = __builtin_amdgcn_perm(0xf6f8fafcu, 0xfdfeff00u, sel);
-    const uint32_t sgn = ((n >> 3) & 0x01010101u) * 0xffu;
-    return (pos & ~sgn) | (neg & sgn);
+    return __builtin_amdgcn_perm(neg, pos, ((n >> 1) & 0x04040404u) | 0x03020100u);
 }
 
 // Q4_K 6-bit scale / min of sub-block j from the 12 scale bytes held as three dwords s[0..2]
