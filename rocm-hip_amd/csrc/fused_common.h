@@ -29,7 +29,7 @@ struct FArgs {
     float* sg;               // scratch [T]
     int8_t* xq;              // scratch: x quantized, Q8_0 values [T][E] and scales [T][E / 32]
     float* xd;
-    int* ids;                // scratch: the routing [T][NU]
+    int* ids;                // scratch: the routing [T][ids_ld] (ids_ld: NU, or NS when the router kernel wrote it)
     float* wts;
     int8_t* act_q;           // scratch [T][NS][FE]
     float* act_d;            // scratch [T][NS][FE / 32]
@@ -50,7 +50,7 @@ struct FArgs {
     float* x_out;
     float eps;
     int norm;
-    int T, E, NE, NU, FE, NS, has_gate;
+    int T, E, NE, NU, FE, NS, has_gate, ids_ld;
 };
 
 // The RMSNorm producer fused into the layer (moe_layer_forward_norm): its arguments
@@ -103,8 +103,12 @@ __device__ __forceinline__ void stamp(const FArgs& a, int k) {
 bool moe_fused_prepare(const moe_layer_desc* d, FArgs& a);
 size_t moe_fused_scratch_bytes(const moe_layer_desc* d, int T);
 char* moe_fused_carve(FArgs& a, void* scratch);
-void moe_fused_carve_q4k(FArgs& a, char* p, qmatvec_q8* qa);  // Q4_K's pieces, from the common part's end
+// Q4_K's pieces, from the common part's end (qx: x's Q8_K bundle, when wanted)
+void moe_fused_carve_q4k(FArgs& a, char* p, qmatvec_q8* qa, qmatvec_q8* qx = nullptr);
 hipError_t moe_fused_launch_down(int type, const FArgs& a, hipStream_t st);  // kernel 3 for a.T tokens
+// Q4_K kernel 3 for a.T tokens from the fp32 gate / up: SwiGLU and the Q8_K input formed inside when FE allows,
+// else the SwiGLU kernel (into qa) and then kernel 3
+hipError_t moe_fused_launch_down_q8k(const FArgs& a, const qmatvec_q8* qa, hipStream_t st);
 void moe_mv_shape(int type, int K, int* lanes, int* units_per_lane);
 unsigned long long* moe_fused_stamps_ptr();  // the table moe_layer_fused_stamps set, or nullptr
 

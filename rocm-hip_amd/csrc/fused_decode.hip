@@ -169,7 +169,7 @@ __global__ void __launch_bounds__(1024) k_fd_down(FArgs a) {
     const int slot = tid >> 6, lane = tid & 63, gl = lane & (L_OUT - 1), i = lane / L_OUT;
     const int i0 = blockIdx.x * RB;
     stamp(a, 5);
-    const int e = slot < NU ? a.ids[t * NU + slot] : -1;
+    const int e = slot < NU ? a.ids[t * a.ids_ld + slot] : -1;
     const long long row = e >= 0 ? (long long)e * E + i0 + i : i0 + i;
     const int mi = e >= 0 ? 2 : 5;
     const uint8_t* vr[1] = {pick(a.v, mi) + row * a.vrb_out};
@@ -193,14 +193,15 @@ __global__ void __launch_bounds__(1024) k_fd_down(FArgs a) {
     stamp(a, 6);
 }
 
-// ---- kernel 3 for Q4_K (T = 1): down's Q8_K input formed here instead of by a SwiGLU launch between kernels 2 and
-// 3. Each slot's wave reads its slot's fp32 gate / up rows (FE = 1024: 16 consecutive values a lane, 16 lanes per
+// ---- kernel 3 for Q4_K, token blockIdx.y (T = 1, or up to 4 tokens after the per-operation id launch of gate / up):
+// down's Q8_K input formed here instead of by a SwiGLU launch before it. Each slot's wave reads its slot's fp32 gate / up rows (FE = 1024: 16 consecutive values a lane, 16 lanes per
 // 256-value block), forms SiLU(g) u (the SwiGLU kernel's expression) and the Q8_K blocks (the quantizer's: the
 // signed value of largest |x| with the lowest index on ties, iscale = -127 / it, q = min(127, rint(iscale x)),
 // d = 1 / iscale, sums of 16), into its own LDS; its weight loads are issued first. Then RS sets of 64 / L_OUT
 // output rows with the per-operation down shape (L_OUT lanes, NUPL_OUT units a lane), and the combine in slot order.
 // The same bits as the SwiGLU kernel and kernel 3; RS row sets a workgroup keep the workgroups' redundant reads of
-// the gate / up rows at E / (RS 64 / L_OUT) x NS x 8 KB.
+// the gate / up rows at E / (RS 64 / L_OUT) x NS x 8 KB per token (RS = 4: 2 and 8 measured slower at T = 1, 8
+// and 16 at T = 2..7).
 #define FD_Q8K_FE 1024
 template <int L_OUT, int NUPL_OUT, int RS>
 __global__ void __launch_bounds__(1024) k_fd_down_q8k(FArgs a) {
@@ -210,11 +211,12 @@ __global__ void __launch_bounds__(1024) k_fd_down_q8k(FArgs a) {
     __shared__ __align__(16) int8_t aq[16][FD_Q8K_FE];
     __shared__ float adk[16][FD_Q8K_FE / 256];
     __shared__ __align__(16) int abk[16][FD_Q8K_FE / 16];
-    const int tid = threadIdx.x, E = a.E, FE = a.FE, NU = a.NU, NS = a.NS;
+    const int tid = threadIdx.x, E = a.E, FE = a.FE, NU = a.NU, NS = a.NS, t = blockIdx.y;
     const int slot = tid >> 6, lane = tid & 63, gl = lane & (L_OUT - 1), i = lane / L_OUT;
     const int i0 = blockIdx.x * RB * RS;
+    const long long sl = (long long)t * NS + slot;  // this (token, slot) pair's gate / up row
     stamp(a, 5);
-    const int e = slot < NU ? a.ids[slot] : -1;
+    const int e = slot < NU ? a.ids[t * a.ids_ld + slot] : -1;
     const int mi = e >= 0 ? 2 : 5;
     const long long rbase = e >= 0 ? (long long)e * E : 0;
     const uint8_t* vb = pick(a.v, mi) + rbase * a.vrb_out;
@@ -229,8 +231,8 @@ __global__ void __launch_bounds__(1024) k_fd_down_q8k(FArgs a) {
             load_packed<QT_Q4_K>(vb + row * a.vrb_out, sb + row * a.srb_out, gl + c * L_OUT, nu_out, wu[r][c]);
     }
     {  // this slot's SwiGLU and Q8_K blocks
-        const float4* g4 = (const float4*)(a.g + (long long)slot * FE + 16 * lane);
-        const float4* u4 = (const float4*)(a.u + (long long)slot * FE + 16 * lane);
+        const float4* g4 = (const float4*)(a.g + sl * FE + 16 * lane);
+        const float4* u4 = (const float4*)(a.u + sl * FE + 16 * lane);
         float v[16];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -282,11 +284,11 @@ __global__ void __launch_bounds__(1024) k_fd_down_q8k(FArgs a) {
     }
     __syncthreads();
     if (tid < RB * RS) {  // the combine kernel's expression
-        const float* wts = a.wts;
+        const float* wts = a.wts + t * NU;
         float o = wts[0] * downv[0][tid];
         for (int j = 1; j < NU; ++j) o += wts[j] * downv[j][tid];
-        if (NS > NU) o += a.has_gate ? downv[NU][tid] * a.sg[0] : downv[NU][tid];
-        a.out[i0 + tid] = o;
+        if (NS > NU) o += a.has_gate ? downv[NU][tid] * a.sg[t] : downv[NU][tid];
+        a.out[(long long)t * E + i0 + tid] = o;
     }
     stamp(a, 6);
 }
@@ -297,6 +299,22 @@ bool moe_packed_planes(const void* W, int type, int K, size_t row_bytes, const u
 
 namespace {
 
+#ifndef FD_Q8K_RS
+#define FD_Q8K_RS 4
+#endif
+
+// Q4_K kernel 3 over a.T rows of workgroups: k_fd_down_q8k when FE is its size, else the SwiGLU kernel and k_fd_down
+template <int LO, int NO>
+hipError_t launch_down_q8k(const FArgs& a, const qmatvec_q8* qa, hipStream_t st) {
+    constexpr int RS = FD_Q8K_RS;  // row sets a workgroup
+    if (a.FE == FD_Q8K_FE && a.E % (RS * (64 / LO)) == 0 && LO * NO * 64 == FD_Q8K_FE)
+        return launch_kernel(k_fd_down_q8k<LO, NO, RS>, dim3(a.E / (RS * (64 / LO)), a.T), dim3(64 * a.NS), 0, st, a);
+    hipError_t e = gpu_swiglu(a.g, a.u, a.act, a.T * a.NS * a.FE, qa, st);
+    if (e == hipSuccess)
+        e = launch_kernel(k_fd_down<QT_Q4_K, LO, NO>, dim3(a.E / (64 / LO), a.T), dim3(64 * a.NS), 0, st, a);
+    return e;
+}
+
 // kernels: bit 0, 1, 2 launch kernel 1, 2 (with Q4_K's SwiGLU), 3 (7 in normal use; a subset only for profiling)
 template <int TYPE, int LI, int NI, int LO, int NO>
 hipError_t launch_fused(const FArgs& a, const qmatvec_q8* qa, int kernels, hipStream_t st) {
@@ -306,17 +324,8 @@ hipError_t launch_fused(const FArgs& a, const qmatvec_q8* qa, int kernels, hipSt
     if (e == hipSuccess && (kernels & 2))
         e = launch_kernel(k_fd_gate_up<TYPE, LI, NI>, dim3(a.NS * (a.FE / 32)), dim3(64 * (64 / FD_GU_RW)), 0, st,
                           a);
-#ifndef FD_Q8K_RS
-#define FD_Q8K_RS 4
-#endif
-    constexpr int RS = FD_Q8K_RS;  // Q4_K: row sets a kernel-3 workgroup
     if constexpr (Fmt<TYPE>::Q8K) {  // down's Q8_K input formed by kernel 3 itself
-        if (e == hipSuccess && (kernels & 4)) {
-            if (a.FE == FD_Q8K_FE && a.E % (RS * (64 / LO)) == 0 && LO * NO * 64 == FD_Q8K_FE)
-                e = launch_kernel(k_fd_down_q8k<LO, NO, RS>, dim3(a.E / (RS * (64 / LO))), dim3(64 * a.NS), 0, st, a);
-            else if ((e = gpu_swiglu(a.g, a.u, a.act, a.NS * a.FE, qa, st)) == hipSuccess)
-                e = launch_kernel(k_fd_down<TYPE, LO, NO>, dim3(a.E / (64 / LO)), dim3(64 * a.NS), 0, st, a);
-        }
+        if (e == hipSuccess && (kernels & 4)) e = launch_down_q8k<LO, NO>(a, qa, st);
         return e;
     }
     if (e == hipSuccess && (kernels & 4))
@@ -383,7 +392,7 @@ size_t moe_fused_scratch_bytes(const moe_layer_desc* d, int T) {
 
 // Q4_K's pieces after the common part (a.T tokens): x's Q8_K bundle [T][E] (kernel 1), gate / up / SwiGLU in
 // fp32 [T][NS][FE] (kernel 2, then the SwiGLU kernel) and down's input bundle [T][NS][FE]; qa receives the latter
-void moe_fused_carve_q4k(FArgs& a, char* p, qmatvec_q8* qa) {
+void moe_fused_carve_q4k(FArgs& a, char* p, qmatvec_q8* qa, qmatvec_q8* qx_out) {
     qmatvec_q8 qx = {};
     const int kx = a.T * ((a.E + 255) / 256 * 256), ka = a.T * a.NS * a.FE;
     qmatvec_q8_bind(&qx, p, kx);
@@ -391,6 +400,7 @@ void moe_fused_carve_q4k(FArgs& a, char* p, qmatvec_q8* qa) {
     qmatvec_q8_bind(qa, p, ka);
     p += fa256(qmatvec_q8_bytes(ka));
     a.xo = {qx.q0, qx.d0, qx.qK, qx.dK, qx.bsK, qx.s0, nullptr, 0};
+    if (qx_out) *qx_out = qx;
     a.g = (float*)p;
     p += fa256((size_t)ka * 4);
     a.u = (float*)p;
@@ -459,6 +469,7 @@ bool moe_fused_prepare(const moe_layer_desc* d, FArgs& a) {
     a.NU = NU;
     a.FE = FE;
     a.NS = NS;
+    a.ids_ld = NU;
     a.w_router = d->w_router;
     a.w_shexp = d->w_shexp;
     a.has_gate = d->s_gate && d->w_shexp ? 1 : 0;
@@ -479,6 +490,13 @@ hipError_t moe_fused_launch(const moe_layer_desc* d, FArgs& a, void* scratch, in
     case QT_ROCMFP4_FAST: return launch_fused_t<QT_ROCMFP4_FAST>(a, &qa, li, ni, lo, no, kernels, st);
     default: return launch_fused_t<QT_Q4_K>(a, &qa, li, ni, lo, no, kernels, st);
     }
+}
+
+hipError_t moe_fused_launch_down_q8k(const FArgs& a, const qmatvec_q8* qa, hipStream_t st) {
+    int lo, no;
+    moe_mv_shape(QT_Q4_K, a.FE, &lo, &no);
+    if (lo == 16 && no == 1) return launch_down_q8k<16, 1>(a, qa, st);
+    return hipErrorInvalidDeviceFunction;
 }
 
 // Kernel 3 for a.T tokens (grid: row blocks x tokens), the multi-token layer's down + combine

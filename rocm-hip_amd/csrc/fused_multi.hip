@@ -469,6 +469,39 @@ hipError_t launch_multi_t(const FArgs& a, const qmatvec_q8* qa, int li, int ni, 
     return hipErrorInvalidDeviceFunction;
 }
 
+size_t q4k_row_bytes(int k) { return (size_t)k / 256 * 144; }
+
+// Q4_K, T = 2..7, per token: kernel 1 (logits, x's Q8_K bundle, shared gates), the router kernel (ids with stride
+// NS, slot NU = -1 when there is a shared expert), the per-operation id launch of gate and up (fp32 [T][NS][FE]),
+// then kernel 3 with the SwiGLU, the Q8_K input and the combine per token
+hipError_t launch_q4k_by_token(const moe_layer_desc* d, FArgs& a, const qmatvec_q8* qx, const qmatvec_q8* qa,
+                               int kernels, hipStream_t st) {
+    hipError_t e = hipSuccess;
+    const int T = a.T, nq = T * (a.E / 256);
+    if (kernels & 1) e = launch_kernel(k_fm_logits, dim3(a.NE + nq + T * a.has_gate), dim3(256), 0, st, a);
+    a.ids_ld = a.NS;
+    if (e == hipSuccess && (kernels & 2)) {
+        const float* lg = a.logits_in ? a.logits_in : a.logits;
+        e = gpu_moe_router(lg, a.x, a.has_gate ? a.w_shexp : nullptr, a.ids, a.wts, a.sg, a.NE, a.NU, a.E, T, st, a.NS);
+        const size_t rb = q4k_row_bytes(a.E);
+        if (e == hipSuccess) {
+            if (a.NS > a.NU)
+                e = qmatvec_launch_q8_id_x(QT_Q4_K, d->w_gate, d->w_up, d->s_gate, d->s_up, rb, a.ids, a.NS, 0, qx,
+                                           a.g, a.u, a.FE, a.E, T, st);
+            else
+                e = qmatvec_launch_q8_id_pair(QT_Q4_K, d->w_gate, d->w_up, rb, a.ids, a.NS, 0, qx, a.g, a.u, a.FE,
+                                              a.E, T, st);
+        }
+    }
+    if (e == hipSuccess && (kernels & 4)) e = moe_fused_launch_down_q8k(a, qa, st);
+    if (e == hipSuccess && (kernels & 2) && a.ids_out)
+        e = hipMemcpy2DAsync(a.ids_out, (size_t)a.NU * 4, a.ids, (size_t)a.NS * 4, (size_t)a.NU * 4, T,
+                             hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess && (kernels & 2) && a.wts_out)
+        e = hipMemcpyAsync(a.wts_out, a.wts, (size_t)T * a.NU * 4, hipMemcpyDeviceToDevice, st);
+    return e;
+}
+
 }  // namespace
 
 static std::atomic<bool> g_fm_q4k{false};  // Q4_K through the multi-token kernels (the parity tests turn it on)
@@ -477,10 +510,7 @@ extern "C" void moe_layer_fused_multi_q4k(int on) { g_fm_q4k.store(on != 0, std:
 // T = 2..FD_MAX_T tokens through the multi-token kernels, when moe_fused_prepare takes the layer
 bool moe_fused_multi_try(const moe_layer_desc* d, const float* x, const float* logits, int T, float* out,
                          int* ids_out, float* wts_out, void* scratch, int kernels, hipStream_t st, hipError_t* err) {
-    // Q4_K: the per-operation path. These kernels are bit-exact for it, but with 256 experts few rows are shared
-    // between tokens and the per-operation id-batch launches read the rows faster (config-3 shape, T = 4: 55.5 us
-    // against 71 us per layer).
-    if (T < 2 || T > FD_MAX_T || (d->type == QT_Q4_K && !g_fm_q4k.load(std::memory_order_relaxed))) return false;
+    if (T < 2 || T > FD_MAX_T) return false;
     FArgs a = {};
     if (!moe_fused_prepare(d, a)) return false;
     if (a.NS > 17 || T * a.NU > 64) return false;  // (the union and the per-token slot tables' sizes)
@@ -492,8 +522,19 @@ bool moe_fused_multi_try(const moe_layer_desc* d, const float* x, const float* l
     a.wts_out = wts_out;
     a.stamps = moe_fused_stamps_ptr();
     char* p = moe_fused_carve(a, scratch);
-    qmatvec_q8 qa = {};
-    if (d->type == QT_Q4_K) moe_fused_carve_q4k(a, p, &qa);
+    qmatvec_q8 qa = {}, qx = {};
+    if (d->type == QT_Q4_K) moe_fused_carve_q4k(a, p, &qa, &qx);
+    // Q4_K: with 256 experts few rows are shared between tokens and the per-operation id launches read each
+    // token's rows faster than the union kernels (config-3 shape, T = 4: 55 us per layer against 65.6), so by
+    // default, up to T = 4, kernel 1, the router kernel, the id launch of gate / up (the shared expert as slot NU)
+    // and the Q4_K kernel 3 -- four launches for the per-operation path's seven, the same bits (config-3 shape:
+    // T = 2 39.5 -> 35.7 us, T = 4 54.7 -> 53.6); from T = 5 the per-operation path (its kernel 3 forms each
+    // token's SwiGLU and Q8_K input in every workgroup: T = 7 76.4 us against 74.5)
+    if (d->type == QT_Q4_K && !g_fm_q4k.load(std::memory_order_relaxed)) {
+        if (T > 4) return false;
+        *err = launch_q4k_by_token(d, a, &qx, &qa, kernels, st);
+        return true;
+    }
     int li, ni, lo, no;
     moe_mv_shape(d->type, a.E, &li, &ni);
     moe_mv_shape(d->type, a.FE, &lo, &no);
