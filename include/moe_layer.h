@@ -67,8 +67,9 @@ void moe_layer_set_fused(int mode);
 // (max(NE + 2, NS * FE / 32, E) always suffices); NULL stops. Launches capture the pointer current at the call.
 void moe_layer_fused_stamps(void* stamps);
 
-// No counterpart in the reference. Whether Q4_K layers at T = 2..7 use the multi-token fused kernels (on != 0)
-// or the per-operation launches (0, the default: faster for Q4_K's shapes); process-wide. Both give the same bits.
+// No counterpart in the reference. Whether Q4_K layers at T = 2..7 use the multi-token union kernels (on != 0)
+// or (0, the default: faster for Q4_K's shapes) four launches per batch up to T = 4 and the per-operation
+// launches beyond; process-wide. All give the same bits.
 void moe_layer_fused_multi_q4k(int on);
 
 #ifdef __cplusplus
