@@ -425,16 +425,12 @@ int orc_max_tiles(int t, int nu, int ne, int tile) {
 }
 
 /* src/gpu_ops.hip:273-320 (moe_group): histogram, exclusive scans of entry and tile counts, the tile table in
- * expert order, and the entries grouped by expert. The reference leaves the order inside an expert's run to
- * its atomics; this oracle fixes it to ascending entry index, which the HIP path also produces. */
-/* Whether entry j of a token's row is the first occurrence of a valid expert id: out-of-range ids and repeats
- * within one row are skipped (the reference's router never produces them; the HIP path skips them too). */
-static int group_valid(const int32_t *row, int j, int ne) {
-    if (row[j] < 0 || row[j] >= ne) return 0;
-    for (int k = 0; k < j; ++k)
-        if (row[k] == row[j]) return 0;
-    return 1;
-}
+ * expert order, and the entries grouped by expert. Every (token, slot) entry is counted and placed, a repeated
+ * id within a token's row included (the reference's histogram at :281 and placement at :316-320 count each
+ * entry). The reference leaves the order inside an expert's run to its atomics; this oracle fixes it to
+ * ascending entry index, which the HIP path also produces. Ids outside [0, ne) are skipped: the reference
+ * indexes its LDS histogram with them unchecked (undefined there), the HIP path skips them too. */
+static int group_valid(const int32_t *row, int j, int ne) { return row[j] >= 0 && row[j] < ne; }
 
 int orc_group(const int32_t *ids, int t, int nu, int ne, int tile, int32_t *counts, int32_t *offsets,
               int32_t *tok_rows, int32_t *pair_rows, int32_t *n_tiles, int32_t *tile_e, int32_t *tile_start,

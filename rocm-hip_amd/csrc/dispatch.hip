@@ -6,12 +6,16 @@
 // reference orders entries inside an expert's run by atomic slot (nondeterministic); here they are in ascending
 // entry order, so the permutation is a pure function of ids.
 //
-// One workgroup of 8 waves; tokens in chunks of 512, one token per lane. Per chunk each wave ORs its lanes into a
-// 64-bit mask per expert in LDS (bit l: lane l's token chose that expert); one thread per expert then turns the
-// masks into counts and into each wave's prefix (the entries of that expert in the chunk's lower waves). Pass 1
-// sums the counts over the chunks (then the scans and the tile table); pass 2 places each entry at its expert's
-// offset + the entries of earlier chunks + its wave's prefix + the popcount of its wave's mask below its lane.
-// A token's repeated id (a malformed row) and ids outside [0, n_expert) are skipped everywhere.
+// One workgroup of 8 waves; tokens in chunks of 512, one token per lane. Every entry of a token's row carries its
+// occurrence index: how many earlier entries of the row hold the same expert id (0 for every entry of a row without
+// repeats). The chunk is processed in levels k = 0 .. (largest occurrence index): at level k each wave ORs its lanes
+// into a 64-bit mask per expert in LDS (bit l: lane l's row holds at least k + 1 entries of that expert); one
+// thread per expert then turns the masks into the wave prefixes and the chunk's count. Summed over the levels, a
+// wave prefix plus the popcount of the wave's mask below a lane is the number of that expert's entries in the
+// chunk's earlier tokens. Pass 1 sums the counts over the chunks (then the scans and the tile table); pass 2
+// places each entry at its expert's first entry + the entries of earlier chunks + that sum + its occurrence index,
+// which is ascending entry order within every expert's run. A row without repeats takes one level: one mask per
+// expert, as a plain histogram would. Ids outside [0, n_expert) are skipped.
 
 #include <atomic>
 
@@ -20,47 +24,78 @@
 #include "moe_common.h"
 
 #define GROUP_WAVES 8
-#define GROUP_MAX_NU 16  // ids of a token held in registers; wider rows read them from memory
 
-// Bit j: entry j of the token's row is the first occurrence of a valid expert id. Rows of at most GROUP_MAX_NU ids
-// are loaded into r at once (unconditional loads: under a per-id branch each one had waited for the previous);
-// wider rows are read from memory.
-__device__ __forceinline__ uint64_t group_valid_mask(const int* row, int nu, int ne, int (&r)[GROUP_MAX_NU]) {
-    uint64_t m = 0;
-    if (nu <= GROUP_MAX_NU) {
+// A token's row in registers: pk[j] = id | occurrence index << 16 for a valid entry, -1 otherwise (and for
+// entries past nu, and for a token past T). NM = 8, 16 or 64: the smallest that holds n_used (<= 64).
+// Returns the row's number of levels (largest occurrence index + 1; 0 for no valid entry). The loads are
+// unconditional within a live row: under a per-id branch each one had waited for the previous.
+template <int NM>
+__device__ __forceinline__ int group_row(const int* row, int nu, int ne, bool live, int (&pk)[NM]) {
+    int r[NM];
 #pragma unroll
-        for (int j = 0; j < GROUP_MAX_NU; ++j) r[j] = row[min(j, nu - 1)];
+    for (int j = 0; j < NM; ++j) r[j] = live ? row[min(j, nu - 1)] : -1;
+    int lv = 0;
 #pragma unroll
-        for (int j = 0; j < GROUP_MAX_NU; ++j) {
-            bool ok = j < nu && r[j] >= 0 && r[j] < ne;
+    for (int j = 0; j < NM; ++j) {
+        const bool ok = j < nu && r[j] >= 0 && r[j] < ne;
+        int occ = 0;
 #pragma unroll
-            for (int k = 0; k < j; ++k) ok = ok && r[k] != r[j];
-            m |= (uint64_t)ok << j;
-        }
-    } else {
-        for (int j = 0; j < nu; ++j) {
-            const int e = row[j];
-            bool ok = e >= 0 && e < ne;
-            for (int k = 0; k < j && ok; ++k) ok = row[k] != e;
-            m |= (uint64_t)ok << j;
-        }
+        for (int k = 0; k < j; ++k) occ += r[k] == r[j] ? 1 : 0;
+        pk[j] = ok ? (r[j] | occ << 16) : -1;
+        lv = ok ? max(lv, occ + 1) : lv;
     }
-    return m;
+    return lv;
 }
 
-// f(j, e) for every valid entry j (bit j of vm) of the row, e its expert id (from r when the row fits it)
-template <typename F>
-__device__ __forceinline__ void for_valid(const int* row, int nu, uint64_t vm, const int (&r)[GROUP_MAX_NU], F f) {
-    if (nu <= GROUP_MAX_NU) {
-#pragma unroll
-        for (int j = 0; j < GROUP_MAX_NU; ++j)
-            if ((vm >> j) & 1) f(j, r[j]);
-    } else {
-        for (int j = 0; j < nu; ++j)
-            if ((vm >> j) & 1) f(j, row[j]);
-    }
+// The largest of the workgroup's lv (LDS word *slot, which the caller set to 0 before a barrier)
+__device__ __forceinline__ int group_levels(int lv, int* slot) {
+    if (lv > 1) atomicMax(slot, lv);
+    __syncthreads();
+    const int l = max(*slot, 1);
+    return l;
 }
 
+// One level of the masks: clears this wave's masks, ORs the lanes whose row has an entry of occurrence index k,
+// then (one thread per expert) the wave prefixes pre[w][e] and the level's count of each expert, added to
+// cnt_add[e] when cnt_add is not null. Ends with a barrier.
+template <int WAVES, int NM>
+__device__ __forceinline__ void group_level(const int (&pk)[NM], int k, int ne, unsigned long long* masks,
+                                            uint16_t* pre, int* cnt_add) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    unsigned long long* my = masks + (size_t)w * ne;
+    for (int e = lane; e < ne; e += 64) my[e] = 0ull;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NM; ++j)
+        if (pk[j] >= 0 && (pk[j] >> 16) == k) atomicOr(&my[pk[j] & 0xffff], 1ull << lane);
+    __syncthreads();
+    for (int e = tid; e < ne; e += 64 * WAVES) {
+        int s = 0;
+#pragma unroll
+        for (int q = 0; q < WAVES; ++q) {
+            pre[(size_t)q * ne + e] = (uint16_t)s;
+            s += __popcll(masks[(size_t)q * ne + e]);
+        }
+        if (cnt_add) cnt_add[e] += s;
+    }
+    __syncthreads();
+}
+
+// acc[j] += the entries of entry j's expert in the lower lanes' and waves' rows at this level (after group_level)
+template <int NM>
+__device__ __forceinline__ void group_accumulate(const int (&pk)[NM], int ne, const unsigned long long* masks,
+                                                 const uint16_t* pre, int (&acc)[NM]) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const unsigned long long below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int j = 0; j < NM; ++j)
+        if (pk[j] >= 0) {
+            const int e = pk[j] & 0xffff;
+            acc[j] += pre[(size_t)w * ne + e] + __popcll(masks[(size_t)w * ne + e] & below);
+        }
+}
+
+template <int NM>
 __global__ void __launch_bounds__(64 * GROUP_WAVES) k_moe_group(const int* ids, int T, int nu, int ne, int tile,
                                                                 int* tok_rows, int* pair_rows, int* n_tiles,
                                                                 int* tile_e, int* tile_start, int* tile_n) {
@@ -71,42 +106,40 @@ __global__ void __launch_bounds__(64 * GROUP_WAVES) k_moe_group(const int* ids, 
     int* cnt = (int*)(pre + (size_t)GROUP_WAVES * ne);             // [ne] entry counts (16 ne bytes in)
     int* eoff = cnt + ne;                                          // [ne] first entry of each expert
     int* run = eoff + ne;                                          // [ne] entries of earlier chunks
+    int* ctot = run + ne;                                          // [ne] entries of the current chunk
     __shared__ int wpart[2][GROUP_WAVES];
+    __shared__ int lvmax;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    unsigned long long* my = masks + (size_t)w * ne;
-    const unsigned long long below = (1ull << lane) - 1ull;
 
-    for (int e = tid; e < ne; e += NT) cnt[e] = run[e] = 0;
+    for (int e = tid; e < ne; e += NT) cnt[e] = run[e] = ctot[e] = 0;
     // pass 0: counts; pass 1: placement
     for (int pass = 0; pass < 2; ++pass) {
         for (int t0 = 0; t0 < T; t0 += NT) {
-            for (int e = lane; e < ne; e += 64) my[e] = 0ull;
+            if (tid == 0) lvmax = 0;
             __syncthreads();
             const int t = t0 + tid;
-            const int* row = ids + (size_t)t * nu;
-            int r[GROUP_MAX_NU];
-            const uint64_t vm = t < T ? group_valid_mask(row, nu, ne, r) : 0ull;
-            for_valid(row, nu, vm, r, [&](int, int e) { atomicOr(&my[e], 1ull << lane); });
-            __syncthreads();
-            for (int e = tid; e < ne; e += NT) {  // prefixes over the waves, the chunk's count
-                int s = 0;
+            int pk[NM], acc[NM];
+            const int levels = group_levels(group_row<NM>(ids + (size_t)t * nu, nu, ne, t < T, pk), &lvmax);
 #pragma unroll
-                for (int k = 0; k < GROUP_WAVES; ++k) {
-                    pre[(size_t)k * ne + e] = (uint16_t)s;
-                    s += __popcll(masks[(size_t)k * ne + e]);
-                }
-                if (pass == 0) cnt[e] += s;
+            for (int j = 0; j < NM; ++j) acc[j] = 0;
+            for (int k = 0; k < levels; ++k) {
+                group_level<GROUP_WAVES, NM>(pk, k, ne, masks, pre, pass == 0 ? cnt : ctot);
+                if (pass == 1) group_accumulate<NM>(pk, ne, masks, pre, acc);
             }
-            __syncthreads();
             if (pass == 1) {
-                for_valid(row, nu, vm, r, [&](int j, int e) {
-                    const int p = eoff[e] + run[e] + pre[(size_t)w * ne + e] + __popcll(my[e] & below);
-                    tok_rows[p] = t;
-                    pair_rows[p] = t * nu + j;
-                });
+#pragma unroll
+                for (int j = 0; j < NM; ++j)
+                    if (pk[j] >= 0) {
+                        const int e = pk[j] & 0xffff;
+                        const int p = eoff[e] + run[e] + acc[j] + (pk[j] >> 16);
+                        tok_rows[p] = t;
+                        pair_rows[p] = t * nu + j;
+                    }
                 __syncthreads();
-                for (int e = tid; e < ne; e += NT)
-                    run[e] += pre[(size_t)(GROUP_WAVES - 1) * ne + e] + __popcll(masks[(size_t)(GROUP_WAVES - 1) * ne + e]);
+                for (int e = tid; e < ne; e += NT) {
+                    run[e] += ctot[e];
+                    ctot[e] = 0;
+                }
             }
             __syncthreads();
         }
@@ -156,39 +189,31 @@ __global__ void __launch_bounds__(64 * GROUP_WAVES) k_moe_group(const int* ids, 
 
 // ---- Several workgroups, with a workspace (gpu_moe_group_ws): the same outputs. Tokens in blocks of 256 (4
 // waves, one token per lane).
-//   k_group_count: per block, the 64-bit expert masks of its 4 waves, then per expert the block's entry count
-//                  into ws[block][expert];
+//   k_group_count: per block, the 64-bit expert masks of its 4 waves level by level, then per expert the block's
+//                  entry count into ws[block][expert];
 //   k_group_place: per block, from the counts: each expert's total and this block's offset within the expert's
 //                  run (the blocks before it), the exclusive scan over the experts (their first entries; block
 //                  0 also scans the tile counts and writes the tile table, k_moe_group's rules); then the masks
-//                  again, the wave prefixes, and each entry's position: the expert's first entry + the block's
-//                  offset + the wave prefix + the popcount of its wave's mask below its lane. (Every block redoes
+//                  again, level by level, and each entry's position: the expert's first entry + the block's
+//                  offset + the summed wave prefixes and popcounts below its lane + its occurrence index. (Every block redoes
 //                  the scans over at most 1,024 experts: cheaper than a launch between the two kernels.)
 #define GB_WAVES 4
 
-__device__ __forceinline__ void block_masks(const int* ids, int T, int nu, int ne, unsigned long long* masks, int t,
-                                            uint64_t& vm, int (&r)[GROUP_MAX_NU]) {
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    unsigned long long* my = masks + (size_t)w * ne;
-    for (int e = lane; e < ne; e += 64) my[e] = 0ull;
-    __syncthreads();
-    const int* row = ids + (size_t)t * nu;
-    vm = t < T ? group_valid_mask(row, nu, ne, r) : 0ull;
-    for_valid(row, nu, vm, r, [&](int, int e) { atomicOr(&my[e], 1ull << lane); });
-    __syncthreads();
-}
-
+template <int NM>
 __global__ void __launch_bounds__(64 * GB_WAVES) k_group_count(const int* ids, int T, int nu, int ne, int* ws) {
     extern __shared__ unsigned long long g_smem[];
-    uint64_t vm;
-    int r[GROUP_MAX_NU];
-    block_masks(ids, T, nu, ne, g_smem, blockIdx.x * 64 * GB_WAVES + threadIdx.x, vm, r);
-    for (int e = threadIdx.x; e < ne; e += 64 * GB_WAVES) {
-        int s = 0;
-#pragma unroll
-        for (int k = 0; k < GB_WAVES; ++k) s += __popcll(g_smem[(size_t)k * ne + e]);
-        ws[(size_t)blockIdx.x * ne + e] = s;
-    }
+    unsigned long long* masks = g_smem;
+    uint16_t* pre = (uint16_t*)(masks + (size_t)GB_WAVES * ne);  // [GB_WAVES][ne]
+    int* bc = (int*)(pre + (size_t)GB_WAVES * ne);                // [ne] the block's counts
+    __shared__ int lvmax;
+    const int tid = threadIdx.x, t = blockIdx.x * 64 * GB_WAVES + tid;
+    for (int e = tid; e < ne; e += 64 * GB_WAVES) bc[e] = 0;
+    if (tid == 0) lvmax = 0;
+    __syncthreads();
+    int pk[NM];
+    const int levels = group_levels(group_row<NM>(ids + (size_t)t * nu, nu, ne, t < T, pk), &lvmax);
+    for (int k = 0; k < levels; ++k) group_level<GB_WAVES, NM>(pk, k, ne, masks, pre, bc);
+    for (int e = tid; e < ne; e += 64 * GB_WAVES) ws[(size_t)blockIdx.x * ne + e] = bc[e];
 }
 
 // Exclusive scan of v[0..n) in place by the 256-thread workgroup (4 consecutive values a thread), n <= 1024;
@@ -222,6 +247,7 @@ __device__ int block256_exscan(int* v, int n, int* part) {
     return total;
 }
 
+template <int NM>
 __global__ void __launch_bounds__(64 * GB_WAVES) k_group_place(const int* ids, int T, int nu, int ne, int tile,
                                                                const int* ws, int nblk, int* tok_rows, int* pair_rows,
                                                                int* n_tiles, int* tile_e, int* tile_start,
@@ -234,7 +260,8 @@ __global__ void __launch_bounds__(64 * GB_WAVES) k_group_place(const int* ids, i
     int* tot = boff + ne;                                         // [ne] block 0: the experts' totals
     int* tsc = tot + ne;                                          // [ne] block 0: tile counts, then first tiles
     __shared__ int part[4];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, t = blockIdx.x * 64 * GB_WAVES + tid;
+    __shared__ int lvmax;
+    const int tid = threadIdx.x, t = blockIdx.x * 64 * GB_WAVES + tid;
     for (int e = tid; e < ne; e += 64 * GB_WAVES) {
         int off = 0, all = 0;
         for (int b = 0; b < nblk; ++b) {
@@ -263,25 +290,24 @@ __global__ void __launch_bounds__(64 * GB_WAVES) k_group_place(const int* ids, i
         }
         if (tid == 0) *n_tiles = nt;
     }
-    uint64_t vm;
-    int r[GROUP_MAX_NU];
-    block_masks(ids, T, nu, ne, masks, t, vm, r);
-    for (int e = tid; e < ne; e += 64 * GB_WAVES) {
-        int s = 0;
-#pragma unroll
-        for (int k = 0; k < GB_WAVES; ++k) {
-            pre[(size_t)k * ne + e] = (uint16_t)s;
-            s += __popcll(masks[(size_t)k * ne + e]);
-        }
-    }
+    int pk[NM], acc[NM];
+    if (tid == 0) lvmax = 0;
     __syncthreads();
-    const int* row = ids + (size_t)t * nu;
-    const unsigned long long below = (1ull << lane) - 1ull;
-    for_valid(row, nu, vm, r, [&](int j, int e) {
-        const int p = eoff[e] + boff[e] + pre[(size_t)w * ne + e] + __popcll(masks[(size_t)w * ne + e] & below);
-        tok_rows[p] = t;
-        pair_rows[p] = t * nu + j;
-    });
+    const int levels = group_levels(group_row<NM>(ids + (size_t)t * nu, nu, ne, t < T, pk), &lvmax);
+#pragma unroll
+    for (int j = 0; j < NM; ++j) acc[j] = 0;
+    for (int k = 0; k < levels; ++k) {
+        group_level<GB_WAVES, NM>(pk, k, ne, masks, pre, nullptr);
+        group_accumulate<NM>(pk, ne, masks, pre, acc);
+    }
+#pragma unroll
+    for (int j = 0; j < NM; ++j)
+        if (pk[j] >= 0) {
+            const int e = pk[j] & 0xffff;
+            const int p = eoff[e] + boff[e] + acc[j] + (pk[j] >> 16);
+            tok_rows[p] = t;
+            pair_rows[p] = t * nu + j;
+        }
 }
 
 extern "C" size_t gpu_moe_group_ws_bytes(int T, int n_expert) {
@@ -300,18 +326,20 @@ extern "C" hipError_t gpu_moe_group_ws(const int* ids, int T, int n_used, int n_
         return hipErrorInvalidValue;
     const int nblk = (T + 64 * GB_WAVES - 1) / (64 * GB_WAVES);
     int* cnt = (int*)ws;
-    const size_t shm_c = (size_t)GB_WAVES * n_expert * 8,
-                 shm_p = shm_c + (size_t)GB_WAVES * n_expert * 2 + 4 * (size_t)n_expert * 4;
-    hipError_t e = launch_kernel(k_group_count, dim3(nblk), dim3(64 * GB_WAVES), shm_c, stream, ids, T, n_used,
-                                 n_expert, cnt);
+    const size_t shm_m = (size_t)GB_WAVES * n_expert * (8 + 2), shm_c = shm_m + (size_t)n_expert * 4,
+                 shm_p = shm_m + 4 * (size_t)n_expert * 4;
+    hipError_t e = launch_kernel(n_used > 16 ? k_group_count<64> : n_used > 8 ? k_group_count<16> : k_group_count<8>,
+                                 dim3(nblk), dim3(64 * GB_WAVES), shm_c, stream, ids, T, n_used, n_expert, cnt);
     if (e == hipSuccess)
-        e = launch_kernel(k_group_place, dim3(nblk), dim3(64 * GB_WAVES), shm_p, stream, ids, T, n_used, n_expert,
-                          tile, (const int*)cnt, nblk, tok_rows, pair_rows, n_tiles, tile_e, tile_start, tile_n);
+        e = launch_kernel(n_used > 16 ? k_group_place<64> : n_used > 8 ? k_group_place<16> : k_group_place<8>,
+                          dim3(nblk), dim3(64 * GB_WAVES), shm_p,
+                          stream, ids, T, n_used, n_expert, tile, (const int*)cnt, nblk, tok_rows, pair_rows, n_tiles,
+                          tile_e, tile_start, tile_n);
     return e;
 }
 
 static size_t group_smem(int ne) {
-    return (size_t)GROUP_WAVES * ne * 8 + (size_t)GROUP_WAVES * ne * 2 + 4 + 3 * (size_t)ne * 4;
+    return (size_t)GROUP_WAVES * ne * 8 + (size_t)GROUP_WAVES * ne * 2 + 4 * (size_t)ne * 4;
 }
 
 extern "C" hipError_t gpu_moe_group(const int* ids, int T, int n_used, int n_expert, int tile, int* tok_rows,
@@ -324,11 +352,12 @@ extern "C" hipError_t gpu_moe_group(const int* ids, int T, int n_used, int n_exp
     const size_t shm = group_smem(n_expert);
     static std::atomic<bool> attr_set{false};  // (setting it twice from racing threads is harmless)
     if (!attr_set.load(std::memory_order_acquire)) {
-        const hipError_t e = hipFuncSetAttribute((const void*)k_moe_group, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)group_smem(1024));
-        if (e != hipSuccess) return e;
+        for (const void* f : {(const void*)k_moe_group<8>, (const void*)k_moe_group<16>, (const void*)k_moe_group<64>}) {
+            const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)group_smem(1024));
+            if (e != hipSuccess) return e;
+        }
         attr_set.store(true, std::memory_order_release);
     }
-    return launch_kernel(k_moe_group, dim3(1), dim3(64 * GROUP_WAVES), shm, stream, ids, T, n_used, n_expert, tile, tok_rows,
-                         pair_rows, n_tiles, tile_e, tile_start, tile_n);
+    return launch_kernel(n_used > 16 ? k_moe_group<64> : n_used > 8 ? k_moe_group<16> : k_moe_group<8>, dim3(1), dim3(64 * GROUP_WAVES), shm, stream,
+                         ids, T, n_used, n_expert, tile, tok_rows, pair_rows, n_tiles, tile_e, tile_start, tile_n);
 }

@@ -127,6 +127,12 @@ class Oracle:
         self.lib.orc_swiglu(_p(g), _p(u), _p(out), g.size)
         return out
 
+    def rmsnorm(self, x, w, eps):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(x)
+        self.lib.orc_rmsnorm(_p(x), _p(None if w is None else np.ascontiguousarray(w, np.float32)), _p(y), x.size, eps)
+        return y
+
     def combine(self, down, wts, shared, sg, nu, n, t):
         out = np.empty(t * n, np.float32)
         self.lib.orc_combine(_p(np.ascontiguousarray(down, np.float32)), _p(np.ascontiguousarray(wts, np.float32)),
@@ -159,6 +165,19 @@ class RefCPU:
         L.qt_row_size.restype, L.qt_row_size.argtypes = _Z, [_I, _L]
         L.ref_rmsnorm.restype, L.ref_rmsnorm.argtypes = None, [_P, _P, _P, _I, _F]
         L.ref_silu.restype, L.ref_silu.argtypes = _F, [_F]
+        L.ref_swiglu.restype, L.ref_swiglu.argtypes = None, [_P, _P, _P, _L]
+
+    def swiglu(self, g, u):
+        g, u = np.ascontiguousarray(g, np.float32), np.ascontiguousarray(u, np.float32)
+        out = np.empty_like(g)
+        self.lib.ref_swiglu(_p(g), _p(u), _p(out), g.size)
+        return out
+
+    def rmsnorm(self, x, w, eps):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(x)
+        self.lib.ref_rmsnorm(_p(x), _p(None if w is None else np.ascontiguousarray(w, np.float32)), _p(y), x.size, eps)
+        return y
 
     def to_float(self, qtype, raw, n):
         out = np.empty(n, np.float32)

@@ -273,11 +273,121 @@ def test_group_invariants(oracle):
         assert g["tile_n"].sum() == t * nu
 
 
-def test_group_skips_invalid(oracle):
+def _group_brute(ids, nu, ne, tile):
+    """moe_group's outputs by brute force (src/gpu_ops.hip:273-320): every entry with an id in [0, ne), repeats
+    within a row included, stably sorted by expert; tiles of each expert's run in expert order."""
+    flat = ids.ravel()
+    ok = (flat >= 0) & (flat < ne)
+    entries = np.flatnonzero(ok)
+    order = entries[np.argsort(flat[entries], kind="stable")]
+    counts = np.bincount(flat[entries], minlength=ne)
+    offs = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    te, ts, tn = [], [], []
+    for e in range(ne):
+        for k in range(0, counts[e], tile):
+            te.append(e), ts.append(offs[e] + k), tn.append(min(tile, counts[e] - k))
+    return dict(counts=counts, pair_rows=order, tok_rows=order // nu, tile_e=te, tile_start=ts, tile_n=tn)
+
+
+def test_group_counts_repeats_and_skips_invalid(oracle):
+    """A repeated id within a token's row is counted and placed twice, as the reference's histogram and atomic
+    placement do (src/gpu_ops.hip:281, 316-320); ids outside [0, ne) are skipped."""
     ids = np.array([[1, 1, 3], [0, 9, -1]], np.int32)  # a repeat, an id past n_expert, a negative id
     g = oracle.group(ids, 2, 3, 4, 2)
-    assert list(g["counts"]) == [1, 1, 0, 1]
-    assert list(g["pair_rows"][:3]) == [3, 0, 2]
+    assert list(g["counts"]) == [1, 2, 0, 1]
+    assert list(g["pair_rows"][:4]) == [3, 0, 1, 2]
+    assert list(g["tok_rows"][:4]) == [1, 0, 0, 0]
+    assert g["n_tiles"] == 3 and list(g["tile_n"][:3]) == [1, 2, 1]
+
+
+@pytest.mark.parametrize("t,nu,ne,tile", [(50, 8, 16, 4), (9, 20, 6, 3), (300, 3, 2, 64), (1, 64, 3, 1)])
+def test_group_repeats_brute_force(oracle, t, nu, ne, tile):
+    rng = np.random.default_rng(t * nu + ne)
+    ids = rng.integers(-1, ne + 1, size=(t, nu)).astype(np.int32)  # many repeats, some invalid ids
+    g = oracle.group(ids, t, nu, ne, tile)
+    b = _group_brute(ids, nu, ne, tile)
+    n = len(b["pair_rows"])
+    assert np.array_equal(g["counts"], b["counts"])
+    assert np.array_equal(g["pair_rows"][:n], b["pair_rows"]) and np.array_equal(g["tok_rows"][:n], b["tok_rows"])
+    assert g["n_tiles"] == len(b["tile_e"])
+    for k in ("tile_e", "tile_start", "tile_n"):
+        assert np.array_equal(g[k][:g["n_tiles"]], b[k]), k
+
+
+# ------------------------------------------------------------------ SwiGLU and RMSNorm
+
+def _special_floats(rng, n):
+    """Random floats across magnitudes plus the special values: +-0, denormals, +-1e+-30, +-88/89 (expf's
+    overflow edge), +-inf."""
+    v = (rng.standard_normal(n) * np.exp(rng.uniform(-20, 20, n))).astype(np.float32)
+    sp = np.array([0.0, -0.0, 1e-40, -1e-40, 1e-30, -1e-30, 1e30, -1e30, 88.0, -88.0, 89.0, -89.0, 100.0, -100.0,
+                   np.inf, -np.inf, 1.0, -1.0, 0.5, -0.5], np.float32)
+    return np.concatenate([v, sp])
+
+
+@needs_ref
+def test_swiglu_matches_reference_silu(oracle, ref):
+    """orc_swiglu == the reference's qwen_silu(g) * u (src/qwen_ops.h:47) bit for bit, special values included."""
+    rng = np.random.default_rng(31)
+    g = _special_floats(rng, 50000)
+    u = np.concatenate([rng.standard_normal(50000).astype(np.float32),
+                        np.array([1, -1, 2, 0, 3, 1e-30, 1e30, -1, 1, 2, -2, 1, -1, 1, 1, 1, 7, -7, 1, 1], np.float32)])
+    a, b = oracle.swiglu(g, u), ref.swiglu(g, u)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    gg = rng.standard_normal(4096).astype(np.float32)
+    assert np.array_equal(oracle.swiglu(gg, np.ones_like(gg)), np.array([ref.lib.ref_silu(float(v)) for v in gg],
+                                                                          np.float32))
+
+
+def test_swiglu_closed_forms(oracle):
+    """SiLU's fixed points: silu(0) = 0; silu(x) = x where e^-x is below half an ulp of 1; g / (1 + e^-g) is NaN at
+    g = -inf (-inf / inf, as in the reference's expression); the float64 value within 3 ulp elsewhere."""
+    one = np.ones(1, np.float32)
+    assert oracle.swiglu(np.zeros(1, np.float32), one)[0] == 0.0
+    big = np.array([30.0, 50.0, 1e6], np.float32)
+    assert np.array_equal(oracle.swiglu(big, np.ones(3, np.float32)), big)
+    assert np.isnan(oracle.swiglu(np.array([-np.inf], np.float32), one)[0])
+    rng = np.random.default_rng(32)
+    g = rng.uniform(-20, 20, 20000).astype(np.float32)
+    u = rng.standard_normal(20000).astype(np.float32)
+    exact = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u
+    got = oracle.swiglu(g, u)
+    assert np.all(np.abs(got - exact) <= 3 * np.spacing(np.abs(exact).astype(np.float32)) + 1e-37)
+
+
+@needs_ref
+@pytest.mark.parametrize("n", [1, 7, 2048, 3072, 4096])
+@pytest.mark.parametrize("with_w", [True, False])
+def test_rmsnorm_matches_reference(oracle, ref, n, with_w):
+    """orc_rmsnorm == the reference's qwen_rmsnorm (src/qwen_ops.cpp:8-13) bit for bit: random rows, rows of
+    zeros, rows at 1e+-30 magnitudes, denormal rows, with and without a weight (w = NULL)."""
+    rng = np.random.default_rng(n)
+    w = rng.standard_normal(n).astype(np.float32) if with_w else None
+    rows = [rng.standard_normal(n).astype(np.float32), np.zeros(n, np.float32),
+            (rng.standard_normal(n) * 1e30).astype(np.float32), (rng.standard_normal(n) * 1e-30).astype(np.float32),
+            np.full(n, 1e-40, np.float32), (rng.standard_normal(n) * 100).astype(np.float32)]
+    for eps in (1e-6, 1e-5, 0.0):
+        for x in rows:
+            a, b = oracle.rmsnorm(x, w, eps), ref.rmsnorm(x, w, eps)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (eps, x[:3])
+
+
+def test_rmsnorm_closed_forms(oracle):
+    """A constant row c maps to c / sqrt(c^2 + eps) (times w); a row of zeros with eps > 0 stays zero; scaling x
+    by a power of two leaves the output unchanged where eps is negligible; float64 agreement within 2 ulp."""
+    n = 2048
+    for c in (1.0, -3.0, 0.25):
+        y = oracle.rmsnorm(np.full(n, c, np.float32), None, 1e-6)
+        assert np.allclose(y, c / np.sqrt(c * c + 1e-6), rtol=2e-7, atol=0)
+    assert not np.any(oracle.rmsnorm(np.zeros(n, np.float32), None, 1e-6))
+    rng = np.random.default_rng(33)
+    x, w = rng.standard_normal(n).astype(np.float32), rng.standard_normal(n).astype(np.float32)
+    a = oracle.rmsnorm(x, w, 0.0)
+    assert np.array_equal(a, oracle.rmsnorm(x * np.float32(64), w, 0.0))
+    x64 = x.astype(np.float64)
+    exact = x64 / np.sqrt(np.mean(x64 * x64) + 1e-5) * w
+    got = oracle.rmsnorm(x, w, 1e-5)
+    assert np.all(np.abs(got - exact) <= 3 * np.spacing(np.abs(exact).astype(np.float32)))
 
 
 # ------------------------------------------------------------------ combine and the layer
