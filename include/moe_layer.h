@@ -55,6 +55,16 @@ hipError_t moe_layer_forward_norm(const moe_layer_desc* d, const float* x_in, co
                                   int* ids_out, float* wts_out, void* scratch, size_t scratch_bytes,
                                   hipStream_t stream);
 
+// No counterpart in the reference: for callers that cannot allocate (code under HIP graph capture, tight serving
+// loops, harnesses that forbid hipMalloc). moe_layer_forward with its scratch in a library-owned device array of
+// MOE_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends) instead of a caller buffer; allocates nothing.
+// Returns hipErrorInvalidValue when moe_layer_scratch_bytes(d, T) exceeds the array (decode T <= 7 of every
+// benchmark configuration fits, and prefill batches up to ~64 tokens). Calls that overlap on one GPU share the
+// array and race: serialize them (one stream, or events between streams).
+#define MOE_NOALLOC_SCRATCH_BYTES (64u << 20)
+hipError_t moe_layer_forward_noalloc(const moe_layer_desc* d, const float* x, const float* logits, int T,
+                                     float* out, int* ids_out, float* wts_out, hipStream_t stream);
+
 // No counterpart in the reference. Whether T == 1 calls may use the fused kernels (1, the default) or always take
 // the per-operation launches (0); process-wide. Profiling only: 0x100 | mask launches just the fused kernels in
 // mask (bit 0: logits / quantize, bit 1: routing + gate / up, bit 2: down + combine), which then read what earlier
