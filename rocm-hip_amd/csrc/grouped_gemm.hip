@@ -94,6 +94,10 @@ struct GArgs {
 #define GG_KB2 4  // the same for the gate / up / SwiGLU kernel (two matrices per stage)
 #endif
 #define GG_NT (GG_TILE / 32)
+#ifndef GG_XCD_RANGES
+#define GG_XCD_RANGES 1  // each XCD takes a contiguous range of work items (0: round-robin, the dispatch order)
+#endif
+#define GG_XCDS 8  // XCDs of an MI355X; workgroup i runs on XCD i % 8
 
 // S = dw (x) dx as one MFMA: lanes 0..31 put their row's / entry's scale in k = 0, every other k is 0
 __device__ __forceinline__ v16f scale_outer(float dw, float dx, int kh) {
@@ -319,8 +323,8 @@ __device__ __forceinline__ void h_compute(const HBuf<NM, KB>& B, const uint4 (&w
 // ------------------------------------------------------------------ the kernel
 
 template <int TYPE, int NM, int KB, int NTU>
-__device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE, NM, KB>::type& buf, int k, int e,
-                                             int st, int cnt, bool shk);
+__device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE, NM, KB>::type& buf, int k, int rb,
+                                             int e, int st, int cnt, bool shk);
 
 // NM = 1: y rows (fp32) of one matrix. NM = 2, SwiGLU: gate (a.v) and up (a.v2) rows of the same block, then
 // act = SiLU(g) u (the swiglu kernel's expression) and its Q8_0 blocks -- a wave's 32 rows of one entry are one
@@ -335,36 +339,51 @@ __attribute__((amdgpu_waves_per_eu(GG_WPE)))
 #endif
 k_grouped(GArgs a) {
     __shared__ __attribute__((aligned(1024))) typename BufOf<TYPE, NM, KB>::type buf;
-    const int k = blockIdx.y;
-    const bool shk = a.vs && k >= a.kr;  // a shared-expert tile
+    // Work items (tile, 128-row block), tile-major, over the tiles that exist: the routed tiles 0 .. n_tiles - 1
+    // (or the dense rows' tiles), then the shared expert's. Each XCD takes one contiguous range of items (the
+    // hardware deals workgroup i to XCD i % 8), so the consecutive tiles of one expert, which read the same
+    // weight rows, run together on one XCD and share its L2 instead of fetching those rows once per XCD.
+    const int nrb = a.N / GG_ROWS;
+    const int nrt = a.n_tiles ? *a.n_tiles : (a.T + GG_TILE - 1) / GG_TILE;  // routed / dense tiles
+    const int nsh = a.vs ? (a.sT + GG_TILE - 1) / GG_TILE : 0;
+    const int items = (nrt + nsh) * nrb;
+#if GG_XCD_RANGES
+    const int per = (items + GG_XCDS - 1) / GG_XCDS, slot = blockIdx.x / GG_XCDS;
+    const int item = (blockIdx.x % GG_XCDS) * per + slot;
+    if (slot >= per || item >= items) return;
+#else
+    const int item = blockIdx.x;
+    if (item >= items) return;
+#endif
+    const int kv = item / nrb, rb = item - kv * nrb;
+    const bool shk = kv >= nrt;  // a shared-expert tile
+    const int k = shk ? a.kr + (kv - nrt) : kv;
     int e, st, cnt;
     if (shk) {
-        st = (k - a.kr) * GG_TILE;
-        if (st >= a.sT) return;
+        st = (kv - nrt) * GG_TILE;
         e = 0;
         cnt = min(GG_TILE, a.sT - st);
     } else if (a.n_tiles) {
-        if (k >= *a.n_tiles) return;
         e = a.tile_e[k];
         st = a.tile_start[k];
         cnt = __builtin_amdgcn_readfirstlane(a.tile_n[k]);
     } else {  // dense: tile k is rows GG_TILE k .. of the one matrix
         st = k * GG_TILE;
-        if (st >= a.T) return;
         e = 0;
         cnt = min(GG_TILE, a.T - st);
     }
     // a tile of at most 32 entries leaves its second 32-entry MFMA tile empty: the loop without it
     if (cnt > 32)
-        grouped_tile<TYPE, NM, KB, GG_NT>(a, buf, k, e, st, cnt, shk);
+        grouped_tile<TYPE, NM, KB, GG_NT>(a, buf, k, rb, e, st, cnt, shk);
     else
-        grouped_tile<TYPE, NM, KB, 1>(a, buf, k, e, st, cnt, shk);
+        grouped_tile<TYPE, NM, KB, 1>(a, buf, k, rb, e, st, cnt, shk);
 }
 
-// One workgroup's tile k (expert e, entries st .. st + cnt - 1) with NTU of its GG_NT 32-entry MFMA tiles in use
+// One workgroup's tile k (expert e, entries st .. st + cnt - 1) and row block rb, with NTU of its GG_NT 32-entry
+// MFMA tiles in use
 template <int TYPE, int NM, int KB, int NTU>
-__device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE, NM, KB>::type& buf, int k, int e,
-                                             int st, int cnt, bool shk) {
+__device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE, NM, KB>::type& buf, int k, int rb,
+                                             int e, int st, int cnt, bool shk) {
     constexpr bool F16 = TYPE != QT_Q8_0;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lr = l & 31, kh = l >> 5;
     auto in_row = [&](int i) { return !shk && a.in_rows ? a.in_rows[st + i] : st + i; };
@@ -372,7 +391,7 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
     const int K = a.K, nb = K / 32;
     // the wave's 32-row group of the stacked matrix (the launcher requires N % 128 == 0 and K % 256 == 0) and
     // this lane's slots in its value and scale tiles (scale slots: 16 bytes per 8 blocks for Q8_0, 32 for FP4)
-    const int r0 = blockIdx.x * GG_ROWS + 32 * w;
+    const int r0 = rb * GG_ROWS + 32 * w;
     const long long grp = ((long long)e * a.N + r0) / 32;
     constexpr int SB = F16 ? 32 : 16;
     constexpr int VS = F16 ? 12 : 16;  // value slot bytes
@@ -488,7 +507,7 @@ bool moe_grouped_mfma_ok(int type, int N, int K) {
 int moe_grouped_mfma_tile(void) { return GG_TILE; }
 
 // The shared-expert tiles of a launch (GArgs::vs ..); sh null: none
-static void bind_shared(GArgs& a, const GShared* sh, int max_tiles, dim3& g) {
+static void bind_shared(GArgs& a, const GShared* sh, int max_tiles, int& tiles) {
     if (!sh) return;
     a.vs = sh->v;
     a.ss = sh->s;
@@ -497,7 +516,13 @@ static void bind_shared(GArgs& a, const GShared* sh, int max_tiles, dim3& g) {
     a.kr = max_tiles;
     a.sT = sh->T;
     a.sout = sh->out0;
-    g.y += (sh->T + GG_TILE - 1) / GG_TILE;
+    tiles += (sh->T + GG_TILE - 1) / GG_TILE;
+}
+
+// A 1-D grid with a workgroup for every (tile, row block) item that can exist, rounded up to whole XCD rounds
+static dim3 grid_of(int N, int tiles) {
+    const long long n = (long long)(N / GG_ROWS) * tiles;
+    return dim3((unsigned)((n + GG_XCDS - 1) / GG_XCDS * GG_XCDS));
 }
 
 hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
@@ -507,8 +532,9 @@ hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s,
                                    hipStream_t stream) {
     GArgs a = {v,      s,       vrb,      srb, q->q0, q->d0, y,       N,       K,       n_tiles, tile_e,
                tile_start, tile_n, in_rows, out_rows, N, 0, nullptr, nullptr, nullptr, nullptr, xt};
-    dim3 g(N / GG_ROWS, max_tiles), b(256);
-    bind_shared(a, sh, max_tiles, g);
+    int tiles = max_tiles;
+    bind_shared(a, sh, max_tiles, tiles);
+    const dim3 g = grid_of(N, tiles), b(256);
     switch (type) {
     case QT_Q8_0: return launch_kernel(k_grouped<QT_Q8_0, 1, GG_KB>, g, b, 0, stream, a);
     case QT_ROCMFP4: return launch_kernel(k_grouped<QT_ROCMFP4, 1, GG_KB>, g, b, 0, stream, a);
@@ -528,8 +554,9 @@ hipError_t moe_launch_grouped_swiglu(int type, const uint8_t* vg, const uint8_t*
                                      hipStream_t stream) {
     GArgs a = {vg,         sg,     vrb,     srb,      q->q0, q->d0, nullptr, N,  K,  n_tiles, tile_e,
                tile_start, tile_n, in_rows, out_rows, N,     0,     vu,      su, aq, ad, xt};
-    dim3 g(N / GG_ROWS, max_tiles), b(256);
-    bind_shared(a, sh, max_tiles, g);
+    int tiles = max_tiles;
+    bind_shared(a, sh, max_tiles, tiles);
+    const dim3 g = grid_of(N, tiles), b(256);
     switch (type) {
     case QT_Q8_0: return launch_kernel(k_grouped<QT_Q8_0, 2, GG_KB2>, g, b, 0, stream, a);
     case QT_ROCMFP4: return launch_kernel(k_grouped<QT_ROCMFP4, 2, GG_KB2>, g, b, 0, stream, a);
@@ -544,7 +571,7 @@ hipError_t moe_launch_dense_mfma(int type, const uint8_t* v, const uint8_t* s, l
                                  hipStream_t stream) {
     GArgs a = {v,       s,       vrb,     srb,     q->q0, q->d0, y,       N,       K,       nullptr, nullptr,
                nullptr, nullptr, nullptr, nullptr, ldy,   T,     nullptr, nullptr, nullptr, nullptr, 0};
-    const dim3 g(N / GG_ROWS, (T + GG_TILE - 1) / GG_TILE), b(256);
+    const dim3 g = grid_of(N, (T + GG_TILE - 1) / GG_TILE), b(256);
     switch (type) {
     case QT_Q8_0: return launch_kernel(k_grouped<QT_Q8_0, 1, GG_KB>, g, b, 0, stream, a);
     case QT_ROCMFP4: return launch_kernel(k_grouped<QT_ROCMFP4, 1, GG_KB>, g, b, 0, stream, a);
