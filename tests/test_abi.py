@@ -69,3 +69,68 @@ def test_no_unresolved_library_symbols():
     out = subprocess.run(["nm", "-D", "--undefined-only", moe_hip.LIB_PATH], capture_output=True, text=True).stdout
     missing = [line.split()[-1] for line in out.splitlines() if " U " in line and "@" not in line]
     assert not missing, missing
+
+
+# ------------------------------------------------------------------ the boundary against the reference's headers
+
+REF_SRC = "/root/reference/src"
+# The section-8(b) boundary: every function a caller of the reference's MoE path binds
+BOUNDARY = ["qmatvec_init", "qmatvec_free", "qmatvec_set_out_scale", "qmatvec_drop_out_scales", "qmatvec_supported",
+            "qmatvec_launch", "qmatvec_launch_batch", "qmatvec_q8_bytes", "qmatvec_q8_bind", "qmatvec_q8_supported",
+            "qmatvec_quantize", "qmatvec_launch_q8", "qmatvec_launch_q8_pair", "qmatvec_launch_q8_batch",
+            "qmatvec_launch_q8_id", "qmatvec_launch_q8_id_pair", "qmatvec_launch_q8_id_x", "qmatvec_id_batch_tile",
+            "qmatvec_q8_id_batch_supported", "qmatvec_launch_q8_id_batch", "gpu_ops_init", "gpu_ops_free",
+            "gpu_add_rmsnorm", "gpu_swiglu", "gpu_moe_router", "gpu_moe_combine", "gpu_moe_combine_scaled",
+            "gpu_moe_max_tiles", "gpu_moe_group"]
+needs_ref_headers = pytest.mark.skipif(not os.path.exists(os.path.join(REF_SRC, "qmatvec.h")),
+                                       reason="the reference tree (its src/qmatvec.h, src/gpu_ops.h) is not present")
+CLANG = "/opt/rocm/llvm/bin/clang++"
+CXXFLAGS = ["-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include"]
+
+
+def _signatures(incdir, tmp_path):
+    """name -> the function type clang gives each boundary declaration in that include directory's headers."""
+    import json
+    src = tmp_path / f"decl_{os.path.basename(incdir)}.cpp"
+    src.write_text('#include "qmatvec.h"\n#include "gpu_ops.h"\n')
+    out = subprocess.run([CLANG, *CXXFLAGS, "-I", incdir, "-fsyntax-only", "-Xclang", "-ast-dump=json", str(src)],
+                         capture_output=True, text=True, check=True).stdout
+    sigs = {}
+
+    def walk(n):
+        if isinstance(n, dict):
+            if n.get("kind") == "FunctionDecl" and n.get("name") in BOUNDARY:
+                sigs[n["name"]] = n["type"]["qualType"]
+            for v in n.get("inner", []):
+                walk(v)
+    walk(json.loads(out))
+    return sigs
+
+
+@needs_ref_headers
+def test_boundary_signatures_match_the_reference_headers(tmp_path):
+    """Every boundary function has the same C type in include/ as in the reference's src/qmatvec.h / gpu_ops.h."""
+    ref = _signatures(REF_SRC, tmp_path)
+    ours = _signatures(os.path.join(ROOT, "include"), tmp_path)
+    assert set(ref) == set(BOUNDARY), set(BOUNDARY) - set(ref)
+    diff = {n: (ref[n], ours.get(n)) for n in BOUNDARY if ref[n] != ours.get(n)}
+    assert not diff, diff
+
+
+@needs_ref_headers
+def test_caller_built_on_the_reference_headers_links_and_runs(tmp_path):
+    """A caller compiled against the reference's headers links against librocm_hip_moe.so and calls every boundary
+    function (no GPU: init fails and every launcher refuses); the same caller compiled against include/ prints the
+    same lines (the qmatvec_q8 layout, the host-side answers, the return codes)."""
+    outs = []
+    for inc in (REF_SRC, os.path.join(ROOT, "include")):
+        exe = tmp_path / f"caller_{len(outs)}"
+        subprocess.run([CLANG, *CXXFLAGS, "-I", inc, os.path.join(ROOT, "tests", "abi_ref", "boundary_caller.cpp"),
+                        "-o", str(exe), "-L", os.path.dirname(moe_hip.LIB_PATH), "-lrocm_hip_moe",
+                        "-Wl,-rpath," + os.path.dirname(moe_hip.LIB_PATH), "-L/opt/rocm/lib", "-lamdhip64"],
+                       check=True, capture_output=True, text=True)
+        r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, r.stderr
+        outs.append(r.stdout)
+    assert outs[0] == outs[1]
+    assert all(line.endswith("= 1") for line in outs[0].splitlines() if "!= " in line or ">= " in line), outs[0]
