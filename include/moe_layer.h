@@ -68,7 +68,10 @@ hipError_t moe_layer_forward_noalloc(const moe_layer_desc* d, const float* x, co
 // No counterpart in the reference. Whether T == 1 calls may use the fused kernels (1, the default) or always take
 // the per-operation launches (0); process-wide. Profiling only: 0x100 | mask launches just the fused kernels in
 // mask (bit 0: logits / quantize, bit 1: routing + gate / up, bit 2: down + combine), which then read what earlier
-// calls left in scratch; a layer's results are undefined in that mode. Other values select 1.
+// calls left in scratch; a layer's results are undefined in that mode. 0x200 | mask (profiling, T >= 8) launches
+// only the prefill stages in mask (bit 0: router logits, quantize, router, dispatch; bit 1: the grouped gate / up /
+// SwiGLU launch; bit 2: the grouped down launch; bit 3: the combine), reading what earlier calls left in scratch;
+// T <= 7 then runs as with 1. Other values select 1.
 void moe_layer_set_fused(int mode);
 
 // No counterpart in the reference (its QWEN_PROFILE times sections on the host). Profiling: every later fused

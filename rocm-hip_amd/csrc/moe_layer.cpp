@@ -109,7 +109,9 @@ Plan plan(const moe_layer_desc* d, int T) {
 }  // namespace
 
 extern "C" void moe_layer_set_fused(int mode) {
-    g_fused.store(mode == 0 || mode == 1 || (mode >= 0x100 && mode <= 0x107) ? mode : 1);
+    g_fused.store(mode == 0 || mode == 1 || (mode >= 0x100 && mode <= 0x107) || (mode >= 0x200 && mode <= 0x20f)
+                      ? mode
+                      : 1);
 }
 
 extern "C" size_t moe_layer_scratch_bytes(const moe_layer_desc* d, int max_t) {
@@ -126,9 +128,12 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
     const int E = d->n_embd, NE = d->n_expert, NU = d->n_used, FE = d->n_ff, type = d->type;
     const bool sh = d->s_gate != nullptr;
     const int mode = g_fused.load(std::memory_order_relaxed);
+    // profiling subsets: 0x100 | mask, the fused decode kernels in mask; 0x200 | mask, the prefill stages in mask
+    // (bit 0: logits, quantize, router, dispatch; 1: grouped gate / up; 2: grouped down; 3: combine)
+    const int pm = (mode & 0x200) ? mode & 0xf : 0xf;
     if (T <= FUSED_MAX_T && mode) {
         hipError_t e = hipSuccess;
-        const int kernels = mode == 1 ? 7 : mode & 7;
+        const int kernels = (mode & 0x100) ? mode & 7 : 7;
         if (T == 1 ? moe_fused_try(d, x, logits_in, out, ids_out, wts_out, scratch, kernels, st, &e, nullptr)
                    : moe_fused_multi_try(d, x, logits_in, T, out, ids_out, wts_out, scratch, kernels, st, &e))
             return e;
@@ -147,15 +152,18 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
     qmatvec_q8_bind(&qx, s + p.qx, p.qx_k);
     qmatvec_q8_bind(&qa, s + p.qa, p.qa_k);
 
+    const bool front = T < 8 || (pm & 1);  // the prefill profiling subsets may leave the front out
     // router logits and routing
     if (logits_in)
         lg = (float*)logits_in;
-    else
+    else if (front)
         CHECK(qmatvec_launch_batch(0, d->w_router, (size_t)E * 4, x, lg, NE, E, T, st));
-    if (type == 12)  // Q4_K reads Q8_K activations; the others read Q8_0 values and scales only
+    if (!front) {
+    } else if (type == 12) {  // Q4_K reads Q8_K activations; the others read Q8_0 values and scales only
         CHECK(qmatvec_quantize(x, T * E, &qx, st));
-    else
+    } else {
         CHECK(moe_quantize_q8_0(x, T * E, &qx, st));
+    }
 
     const bool slot = T == 1 && sh;  // moe_core_one: the shared expert as slot NU
     bool shared_done = false;  // the prefill path ran the shared expert and the combine with the routed experts
@@ -179,15 +187,16 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
             CHECK(gpu_moe_combine(down, wts, nullptr, nullptr, out, NU, E, T, st));
         }
     } else {
-        CHECK(gpu_moe_router(lg, x, d->w_shexp, ids, wts, sg, NE, NU, E, T, st, NU));
+        if (pm & 1) CHECK(gpu_moe_router(lg, x, d->w_shexp, ids, wts, sg, NE, NU, E, T, st, NU));
         int* tok = (int*)(s + p.tok);
         int* pair = (int*)(s + p.pair);
         int* ntile = (int*)(s + p.ntile);
         int* te = (int*)(s + p.te);
         int* ts = (int*)(s + p.ts);
         int* tn = (int*)(s + p.tn);
-        CHECK(gpu_moe_group_ws(ids, T, NU, NE, p.tile, tok, pair, ntile, te, ts, tn, s + p.gws,
-                               gpu_moe_group_ws_bytes(T, NE), st));
+        if (pm & 1)
+            CHECK(gpu_moe_group_ws(ids, T, NU, NE, p.tile, tok, pair, ntile, te, ts, tn, s + p.gws,
+                                   gpu_moe_group_ws_bytes(T, NE), st));
         const uint8_t *vg = nullptr, *sgp = nullptr, *vu = nullptr, *sup = nullptr, *vd = nullptr, *sdp = nullptr;
         long long gvs = 0, gss = 0, dvs = 0, dss = 0;  // tile bytes per 32-row group (gate and up alike, down)
         if (mode && moe_grouped_mfma_ok(type, FE, E) && moe_grouped_mfma_ok(type, E, FE) &&
@@ -205,12 +214,16 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
             shg.out0 = shd.out0 = (long long)T * NU;
             // gate, up, SwiGLU and down's Q8_0 input in one launch (the same bits as the three launches below); the
             // input handed to down in entry-tile order
-            CHECK(moe_launch_grouped_swiglu(type, vg, sgp, vu, sup, gvs, gss,
-                                            &qx, qa.q0, qa.d0, FE, E, p.max_tiles, ntile, te, ts, tn, tok, pair,
-                                            2 /* down's input in entry-tile order */, merged ? &shg : nullptr, st));
-            CHECK(moe_launch_grouped_mfma(type, vd, sdp, dvs, dss, &qa, down,
-                                          E, FE, p.max_tiles, ntile, te, ts, tn, nullptr, pair,
-                                          1 /* input in entry-tile order */, merged ? &shd : nullptr, st));
+            if (pm & 2)
+                CHECK(moe_launch_grouped_swiglu(type, vg, sgp, vu, sup, gvs, gss, &qx, qa.q0, qa.d0, FE, E,
+                                                p.max_tiles, ntile, te, ts, tn, tok, pair,
+                                                2 /* down's input in entry-tile order */, merged ? &shg : nullptr,
+                                                st));
+            if (pm & 4)
+                CHECK(moe_launch_grouped_mfma(type, vd, sdp, dvs, dss, &qa, down, E, FE, p.max_tiles, ntile, te, ts,
+                                              tn, nullptr, pair, 1 /* input in entry-tile order */,
+                                              merged ? &shd : nullptr, st));
+            if (!(pm & 8)) return hipSuccess;
             if (merged) {
                 CHECK(gpu_moe_combine(down, wts, down + (size_t)T * NU * E, d->w_shexp ? sg : nullptr, out, NU, E, T,
                                       st));
