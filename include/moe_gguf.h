@@ -41,7 +41,8 @@ typedef struct moe_gguf_layer {
 int moe_gguf_layer_bind(const gguf_model_t* model, int layer, moe_layer_desc* desc);
 
 // Bind, then copy the layer's tensors into one device allocation (through pinned staging buffers, on stream) and,
-// with pack set, register gate, up, down and the shared expert with qmatvec_pack_weights so that
+// with pack set, register gate, up, down and the shared expert with qmatvec_pack_weights_ex (flags pack - 1:
+// 1 the default copy and tiles, 2 in place, 3 a copy without tiles, 4 in place without tiles) so that
 // moe_layer_forward takes its fused and MFMA paths. Synchronous: returns once the copies are done. On failure
 // nothing stays allocated: hipErrorInvalidValue for a binding error (moe_gguf_error()), else the HIP error.
 hipError_t moe_gguf_layer_upload(const gguf_model_t* model, int layer, int pack, moe_gguf_layer* out,

@@ -118,8 +118,9 @@ __global__ void __launch_bounds__(256) k_expert_entries(MvArgs a, const int* n_t
 
 // ------------------------------------------------------------------ split-plane copies
 
-// One thread per native block (32 values; 256 for Q4_K)
-template <int TYPE>
+// One thread per native block (32 values; 256 for Q4_K). UNPACK = false: native rows W -> planes V / S; true: the
+// inverse (planes -> native rows, for unregistering a matrix packed in place)
+template <int TYPE, bool UNPACK = false>
 __global__ void __launch_bounds__(256) k_pack(const uint8_t* W, long long row_bytes, long long rows, int K, uint8_t* V,
                                               uint8_t* S) {
     constexpr int BV = TYPE == QT_Q4_K ? 256 : 32, BB = Fmt<TYPE>::BLOCK_BYTES;
@@ -128,31 +129,38 @@ __global__ void __launch_bounds__(256) k_pack(const uint8_t* W, long long row_by
     if (i >= rows * nb) return;
     const long long r = i / nb;
     const int b = (int)(i - r * nb);
-    const uint8_t* src = W + r * row_bytes + (long long)b * BB;
+    uint8_t* src = (uint8_t*)W + r * row_bytes + (long long)b * BB;
     uint8_t* vr = V + r * fmt_value_row(TYPE, K);
     uint8_t* sr = S + r * fmt_scale_row(TYPE, K);
+    // moves one byte between its native place n and its plane place p, in the direction of UNPACK
+    auto mv = [](uint8_t& n, uint8_t& p) {
+        if constexpr (UNPACK)
+            n = p;
+        else
+            p = n;
+    };
     if constexpr (TYPE == QT_Q8_0) {
-        sr[2 * b] = src[0];
-        sr[2 * b + 1] = src[1];
+        mv(src[0], sr[2 * b]);
+        mv(src[1], sr[2 * b + 1]);
         for (int j = 0; j < 16; ++j) {
-            vr[16 * b + j] = src[2 + j];
-            vr[16 * (nb + b) + j] = src[18 + j];
+            mv(src[2 + j], vr[16 * b + j]);
+            mv(src[18 + j], vr[16 * (nb + b) + j]);
         }
     } else if constexpr (TYPE == QT_ROCMFP4) {
-        for (int j = 0; j < 16; ++j) vr[16 * b + j] = src[j];
-        sr[2 * b] = src[16];
-        sr[2 * b + 1] = src[17];
+        for (int j = 0; j < 16; ++j) mv(src[j], vr[16 * b + j]);
+        mv(src[16], sr[2 * b]);
+        mv(src[17], sr[2 * b + 1]);
     } else if constexpr (TYPE == QT_ROCMFP4_FAST) {
-        for (int j = 0; j < 16; ++j) vr[16 * b + j] = src[j];
-        sr[b] = src[16];
+        for (int j = 0; j < 16; ++j) mv(src[j], vr[16 * b + j]);
+        mv(src[16], sr[b]);
     } else {  // Q4_K: head -> scale plane, chunk c (32 value bytes) -> unit 4b + c in the two half planes
         const int nu = K / 64;
-        for (int j = 0; j < 16; ++j) sr[16 * b + j] = src[j];
+        for (int j = 0; j < 16; ++j) mv(src[j], sr[16 * b + j]);
         for (int c = 0; c < 4; ++c) {
             const int u = 4 * b + c;
             for (int j = 0; j < 16; ++j) {
-                vr[16 * u + j] = src[16 + 32 * c + j];
-                vr[16 * (nu + u) + j] = src[16 + 32 * c + 16 + j];
+                mv(src[16 + 32 * c + j], vr[16 * u + j]);
+                mv(src[16 + 32 * c + 16 + j], vr[16 * (nu + u) + j]);
             }
         }
     }
@@ -235,8 +243,10 @@ struct Packed {
     int type, K;
     size_t row_bytes;
     long long rows;
-    uint8_t* mem;    // value plane, then scale plane
+    uint8_t* mem;    // value plane, then scale plane (packed in place: the native buffer W itself)
     uint8_t* tiles;  // MFMA operand tiles (value tiles, then scale tiles), or nullptr
+    bool inplace;    // the planes replaced the native rows in W
+    uint8_t* alloc;  // the device memory the registration allocated (planes and / or tiles), or nullptr
 };
 
 // Whether a registered matrix also gets MFMA operand tiles: a type of the MFMA kernels, whole 32-row groups and
@@ -375,21 +385,34 @@ hipError_t launch_mv(int type, bool packed, const MvArgs& a, dim3 yz, int nrows,
     return hipErrorInvalidDeviceFunction;
 }
 
+// Whether the registered matrix covering W (if any) was packed in place: its native rows are gone
+bool packed_in_place(const void* W) {
+    std::lock_guard<std::mutex> lk(g_pack_mu);
+    auto it = g_packed.upper_bound((uintptr_t)W);
+    if (it == g_packed.begin()) return false;
+    --it;
+    return (uintptr_t)W < it->second.end && it->second.inplace;
+}
+
 // Fill the weight side of a: every non-null matrix from its split-plane copy if all of them have one, else all
-// native. Returns whether the copies are used.
-bool bind_weights(MvArgs& a, int type, int K, size_t row_bytes, const void* const W[4]) {
+// native. Returns 1 when the copies are used, 0 for native rows, -1 when the matrices cannot be read together (one
+// packed in place, which has no native rows left, with one that is not registered for this shape).
+int bind_weights(MvArgs& a, int type, int K, size_t row_bytes, const void* const W[4]) {
     const uint8_t* v[4] = {nullptr, nullptr, nullptr, nullptr};
     const uint8_t* s[4] = {nullptr, nullptr, nullptr, nullptr};
     bool all = true;
     for (int i = 0; i < 4; ++i)
         if (W[i] && !find_packed(W[i], type, K, row_bytes, &v[i], &s[i])) all = false;
+    if (!all)
+        for (int i = 0; i < 4; ++i)
+            if (W[i] && packed_in_place(W[i])) return -1;
     for (int i = 0; i < 4; ++i) {
         a.v[i] = all ? v[i] : (const uint8_t*)W[i];
         a.s[i] = all ? s[i] : nullptr;
     }
     a.vrb = all ? fmt_value_row(type, K) : (long long)row_bytes;
     a.srb = all ? fmt_scale_row(type, K) : 0;
-    return all;
+    return all ? 1 : 0;
 }
 
 void bind_acts(MvArgs& a, int type, const qmatvec_q8* q) {
@@ -431,24 +454,64 @@ static hipError_t launch_pack(const void* W, size_t rb, long long rows, int K, u
     const long long n = rows * (K / BV);
     uint8_t* V = mem;
     uint8_t* S = mem + (size_t)rows * fmt_value_row(TYPE, K);
-    hipError_t e = launch_kernel(k_pack<TYPE>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                                 (const uint8_t*)W, (long long)rb, rows, K, V, S);
-    if constexpr (TYPE != QT_Q4_K) {
-        if (e == hipSuccess && tiles) {
+    hipError_t e = hipSuccess;
+    if constexpr (TYPE != QT_Q4_K) {  // the tiles first: an in-place registration overwrites W after them
+        if (tiles) {
             const long long nt = rows / 32 * (K / 32) * 64 + rows * (K / 256);
             e = launch_kernel(k_pack_tiles<TYPE>, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st,
                               (const uint8_t*)W, (long long)rb, rows, K, tiles,
                               tiles + (size_t)rows * tile_value_row(TYPE, K));  // scale tiles after the values
         }
     }
+    if (e == hipSuccess)
+        e = launch_kernel(k_pack<TYPE, false>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                          (const uint8_t*)W, (long long)rb, rows, K, V, S);
     return e;
 }
 
-extern "C" hipError_t qmatvec_pack_weights(int type, const void* W, size_t row_bytes, long long rows, int K,
-                                           hipStream_t stream) {
+template <int TYPE>
+static hipError_t launch_unpack(uint8_t* W, size_t rb, long long rows, int K, uint8_t* planes, hipStream_t st) {
+    constexpr int BV = TYPE == QT_Q4_K ? 256 : 32;
+    const long long n = rows * (K / BV);
+    return launch_kernel(k_pack<TYPE, true>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const uint8_t*)W,
+                         (long long)rb, rows, K, planes, planes + (size_t)rows * fmt_value_row(TYPE, K));
+}
+
+static hipError_t pack_type(int type, const void* W, size_t rb, long long rows, int K, uint8_t* planes, uint8_t* tiles,
+                            hipStream_t st) {
+    switch (type) {
+    case QT_Q8_0: return launch_pack<QT_Q8_0>(W, rb, rows, K, planes, tiles, st);
+    case QT_ROCMFP4: return launch_pack<QT_ROCMFP4>(W, rb, rows, K, planes, tiles, st);
+    case QT_ROCMFP4_FAST: return launch_pack<QT_ROCMFP4_FAST>(W, rb, rows, K, planes, tiles, st);
+    default: return launch_pack<QT_Q4_K>(W, rb, rows, K, planes, nullptr, st);
+    }
+}
+
+static hipError_t unpack_type(int type, uint8_t* W, size_t rb, long long rows, int K, uint8_t* planes, hipStream_t st) {
+    switch (type) {
+    case QT_Q8_0: return launch_unpack<QT_Q8_0>(W, rb, rows, K, planes, st);
+    case QT_ROCMFP4: return launch_unpack<QT_ROCMFP4>(W, rb, rows, K, planes, st);
+    case QT_ROCMFP4_FAST: return launch_unpack<QT_ROCMFP4_FAST>(W, rb, rows, K, planes, st);
+    default: return launch_unpack<QT_Q4_K>(W, rb, rows, K, planes, st);
+    }
+}
+
+static size_t tile_bytes_of(int type, long long rows, int K, int flags) {
+    if ((flags & QMATVEC_PACK_NO_TILES) || !tiles_ok(type, rows, K)) return 0;
+    return (size_t)rows * (size_t)(tile_value_row(type, K) + tile_scale_row(type, K));
+}
+
+extern "C" size_t qmatvec_registered_bytes(int type, long long rows, int K, int flags) {
+    if (!qmatvec_q8_supported(type, K) || rows <= 0 || (flags & ~3)) return 0;
+    return ((flags & QMATVEC_PACK_INPLACE) ? 0 : packed_planes_bytes(type, rows, K)) +
+           tile_bytes_of(type, rows, K, flags);
+}
+
+extern "C" hipError_t qmatvec_pack_weights_ex(int type, void* W, size_t row_bytes, long long rows, int K, int flags,
+                                              hipStream_t stream) {
     if (!moe_lib_ready()) return hipErrorNotInitialized;
     if (!qmatvec_q8_supported(type, K)) return hipErrorInvalidDeviceFunction;
-    if (!W || rows <= 0 || row_bytes != native_row(type, K)) return hipErrorInvalidValue;
+    if (!W || rows <= 0 || row_bytes != native_row(type, K) || (flags & ~3)) return hipErrorInvalidValue;
     const size_t bytes = row_bytes * (size_t)rows;
     {
         std::lock_guard<std::mutex> lk(g_pack_mu);
@@ -456,40 +519,74 @@ extern "C" hipError_t qmatvec_pack_weights(int type, const void* W, size_t row_b
         if (it != g_packed.end() && it->first < (uintptr_t)W + bytes) return hipErrorInvalidValue;  // overlap
         if (it != g_packed.begin() && std::prev(it)->second.end > (uintptr_t)W) return hipErrorInvalidValue;
     }
-    const size_t planes = packed_planes_bytes(type, rows, K);
-    const bool tiled = tiles_ok(type, rows, K);
-    const size_t tile_bytes = tiled ? (size_t)rows * (size_t)(tile_value_row(type, K) + tile_scale_row(type, K)) : 0;
-    void* mem = nullptr;
-    hipError_t e = hipMalloc(&mem, planes + tile_bytes);
-    if (e != hipSuccess) return e;
-    uint8_t* m8 = (uint8_t*)mem;
-    uint8_t* tiles = tiled ? m8 + planes : nullptr;
-    switch (type) {
-    case QT_Q8_0: e = launch_pack<QT_Q8_0>(W, row_bytes, rows, K, m8, tiles, stream); break;
-    case QT_ROCMFP4: e = launch_pack<QT_ROCMFP4>(W, row_bytes, rows, K, m8, tiles, stream); break;
-    case QT_ROCMFP4_FAST: e = launch_pack<QT_ROCMFP4_FAST>(W, row_bytes, rows, K, m8, tiles, stream); break;
-    default: e = launch_pack<QT_Q4_K>(W, row_bytes, rows, K, m8, nullptr, stream); break;
+    const bool inplace = flags & QMATVEC_PACK_INPLACE;
+    const size_t planes = packed_planes_bytes(type, rows, K);  // (== bytes: the planes hold the native bytes)
+    const size_t tile_bytes = tile_bytes_of(type, rows, K, flags);
+    const size_t keep = (inplace ? 0 : planes) + tile_bytes;  // what the registration holds
+    uint8_t* alloc = nullptr;
+    if (keep) {
+        void* m = nullptr;
+        const hipError_t e = hipMalloc(&m, keep);
+        if (e != hipSuccess) return e;
+        alloc = (uint8_t*)m;
+    }
+    uint8_t* tiles = tile_bytes ? alloc + (inplace ? 0 : planes) : nullptr;
+    hipError_t e = hipSuccess;
+    if (!inplace) {
+        e = pack_type(type, W, row_bytes, rows, K, alloc, tiles, stream);
+    } else {
+        // the planes go to a transient buffer (a block's native bytes and its plane bytes overlap other blocks'),
+        // then over W; the call waits for the copy so that the transient buffer can be freed
+        void* tmp = nullptr;
+        e = hipMalloc(&tmp, planes);
+        if (e == hipSuccess) {
+            e = pack_type(type, W, row_bytes, rows, K, (uint8_t*)tmp, tiles, stream);
+            if (e == hipSuccess) e = hipMemcpyAsync(W, tmp, planes, hipMemcpyDeviceToDevice, stream);
+            const hipError_t es = hipStreamSynchronize(stream);
+            if (e == hipSuccess) e = es;
+            (void)hipFree(tmp);
+        }
     }
     if (e != hipSuccess) {
-        (void)hipFree(mem);
+        if (alloc) {
+            (void)hipStreamSynchronize(stream);
+            (void)hipFree(alloc);
+        }
         return e;
     }
     std::lock_guard<std::mutex> lk(g_pack_mu);
-    g_packed[(uintptr_t)W] = Packed{(uintptr_t)W + bytes, type, K, row_bytes, rows, m8, tiles};
+    g_packed[(uintptr_t)W] = Packed{(uintptr_t)W + bytes, type, K, row_bytes, rows,
+                                    inplace ? (uint8_t*)W : alloc, tiles, inplace, alloc};
     return hipSuccess;
 }
 
+extern "C" hipError_t qmatvec_pack_weights(int type, const void* W, size_t row_bytes, long long rows, int K,
+                                           hipStream_t stream) {
+    return qmatvec_pack_weights_ex(type, (void*)W, row_bytes, rows, K, 0, stream);
+}
+
 extern "C" void qmatvec_unpack_weights(const void* W) {
-    uint8_t* mem = nullptr;
+    Packed p;
     {
         std::lock_guard<std::mutex> lk(g_pack_mu);
         auto it = g_packed.find((uintptr_t)W);
         if (it == g_packed.end()) return;
-        mem = it->second.mem;
+        p = it->second;
         g_packed.erase(it);
     }
-    // launches already queued on any stream may still read the copy
-    if (hipDeviceSynchronize() == hipSuccess) (void)hipFree(mem);
+    // launches already queued on any stream may still read the copy (or, packed in place, W's planes)
+    if (hipDeviceSynchronize() != hipSuccess) return;
+    if (p.inplace) {  // the native rows back into W, through a transient copy of the planes
+        const size_t planes = packed_planes_bytes(p.type, p.rows, p.K);
+        void* tmp = nullptr;
+        if (hipMalloc(&tmp, planes) == hipSuccess) {
+            if (hipMemcpy(tmp, W, planes, hipMemcpyDeviceToDevice) == hipSuccess &&
+                unpack_type(p.type, (uint8_t*)W, p.row_bytes, p.rows, p.K, (uint8_t*)tmp, nullptr) == hipSuccess)
+                (void)hipDeviceSynchronize();
+            (void)hipFree(tmp);
+        }
+    }
+    if (p.alloc) (void)hipFree(p.alloc);
 }
 
 // The per-operation kernels' lane shape for a row of K values (the fused layer kernel copies it)
@@ -519,7 +616,8 @@ void moe_unpack_all(void) {
     }
     if (all.empty()) return;
     (void)hipDeviceSynchronize();
-    for (auto& kv : all) (void)hipFree(kv.second.mem);
+    for (auto& kv : all)
+        if (kv.second.alloc) (void)hipFree(kv.second.alloc);
 }
 
 static hipError_t check_common(int type, const void* W, size_t row_bytes, const qmatvec_q8* q, int K,
@@ -545,7 +643,9 @@ extern "C" hipError_t qmatvec_launch_q8_id_x(int type, const void* W, const void
     if (!aligned(W2, 4) || !aligned(Wx, 4) || !aligned(W2x, 4)) return hipErrorInvalidValue;
     MvArgs a = {};
     const void* Ws[4] = {W, W2, Wx, W2 ? W2x : nullptr};
-    const bool packed = bind_weights(a, type, K, row_bytes, Ws);
+    const int bw = bind_weights(a, type, K, row_bytes, Ws);
+    if (bw < 0) return hipErrorInvalidValue;
+    const bool packed = bw > 0;
     bind_acts(a, type, q);
     a.ids = ids;
     a.n_used = n_used;
@@ -581,7 +681,9 @@ static hipError_t dense(int type, const void* W, int N, float* y, const void* W2
     if (!aligned(W2, 4)) return hipErrorInvalidValue;
     MvArgs a = {};
     const void* Ws[4] = {W, W2, nullptr, nullptr};
-    const bool packed = bind_weights(a, type, K, row_bytes, Ws);
+    const int bw = bind_weights(a, type, K, row_bytes, Ws);
+    if (bw < 0) return hipErrorInvalidValue;
+    const bool packed = bw > 0;
     bind_acts(a, type, q);
     a.ids = nullptr;
     a.n_used = 1;
@@ -632,7 +734,9 @@ hipError_t moe_launch_entries(int type, const void* W, size_t row_bytes, const q
                               hipStream_t stream) {
     MvArgs a = {};
     const void* Ws[4] = {W, nullptr, nullptr, nullptr};
-    const bool packed = bind_weights(a, type, K, row_bytes, Ws);
+    const int bw = bind_weights(a, type, K, row_bytes, Ws);
+    if (bw < 0) return hipErrorInvalidValue;
+    const bool packed = bw > 0;
     bind_acts(a, type, q);
     a.N = a.N2 = N;
     a.ldy = N;

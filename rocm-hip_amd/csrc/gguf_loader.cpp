@@ -769,13 +769,14 @@ hipError_t moe_gguf_layer_upload(const gguf_model_t* g, int layer, int pack, moe
     const void* p[8];
     for (int i = 0; i < 8; ++i) p[i] = parts[i]->bytes ? (const char*)out->dev + off[i] : nullptr;
     fill_desc(b, &out->desc, p);
+    if (e == hipSuccess && (pack < 0 || pack > 4)) e = hipErrorInvalidValue;
     if (e == hipSuccess && pack) {
         out->packed = 1;
         const Bound* mats[6] = {&b.gate, &b.up, &b.down, &b.sgate, &b.sup, &b.sdown};
         for (int i = 0; i < 6 && e == hipSuccess; ++i)
             if (mats[i]->bytes)
-                e = qmatvec_pack_weights(mats[i]->type, p[1 + i], row_bytes(mats[i]->type, mats[i]->K), mats[i]->N,
-                                         (int)mats[i]->K, stream);
+                e = qmatvec_pack_weights_ex(mats[i]->type, (void*)p[1 + i], row_bytes(mats[i]->type, mats[i]->K),
+                                            mats[i]->N, (int)mats[i]->K, pack - 1, stream);
         if (e == hipSuccess) e = hipStreamSynchronize(stream);
     }
     if (e != hipSuccess) {

@@ -63,6 +63,8 @@ SIGNATURES = {
     "qmatvec_launch_q8_id_batch": (_I, [_I, _P, _Z, _Q8P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "qmatvec_pack_weights": (_I, [_I, _P, _Z, _L, _I, _P]),
     "qmatvec_unpack_weights": (None, [_P]),
+    "qmatvec_pack_weights_ex": (_I, [_I, _P, _Z, _L, _I, _I, _P]),
+    "qmatvec_registered_bytes": (_Z, [_I, _L, _I, _I]),
     "qmatvec_packed_bytes": (_Z, [_I, _L, _I]),
     "gpu_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _Q8P, _P]),
     "gpu_swiglu": (_I, [_P, _P, _P, _I, _Q8P, _P]),

@@ -134,3 +134,17 @@ def test_caller_built_on_the_reference_headers_links_and_runs(tmp_path):
         outs.append(r.stdout)
     assert outs[0] == outs[1]
     assert all(line.endswith("= 1") for line in outs[0].splitlines() if "!= " in line or ">= " in line), outs[0]
+
+
+def test_registered_bytes_per_mode():
+    """Device bytes a registration allocates besides W: the copy (native size) unless in place, the tiles (Q8_0: the
+    native size; FP4: 0.75 K + K / 8 bytes per row) unless left out or the shape has none (Q4_K)."""
+    lib = moe_hip.load_library()
+    rows, K = 128 * 768, 2048
+    for t, rb, tile_row in ((8, 2176, 2048 + 128), (100, 1152, 1536 + 256), (12, 1152, 0)):
+        native = rows * rb
+        assert lib.qmatvec_registered_bytes(t, rows, K, 0) == native + rows * tile_row
+        assert lib.qmatvec_registered_bytes(t, rows, K, 1) == rows * tile_row
+        assert lib.qmatvec_registered_bytes(t, rows, K, 2) == native
+        assert lib.qmatvec_registered_bytes(t, rows, K, 3) == 0
+    assert lib.qmatvec_registered_bytes(8, rows, K, 4) == 0 and lib.qmatvec_registered_bytes(2, rows, K, 0) == 0
