@@ -158,6 +158,42 @@ def load_library(path=LIB_PATH):
     return lib
 
 
+ENGINE_PATH = os.path.join(HERE, "libmoe_ffn_engine.so")
+
+
+class EngineWeight(ctypes.Structure):
+    """struct moe_engine_weight (include/moe_ffn_engine.h)."""
+    _fields_ = [("type", _I), ("data", _P), ("row_bytes", _Z), ("N", _I), ("K", _I)]
+
+
+class EngineLayer(ctypes.Structure):
+    """struct moe_engine_layer (include/moe_ffn_engine.h)."""
+    _fields_ = [("n_embd", _I), ("n_expert", _I), ("n_used", _I), ("n_ff_exp", _I), ("n_ff_shexp", _I),
+                ("router", EngineWeight), ("exp_gate", EngineWeight), ("exp_up", EngineWeight),
+                ("exp_down", EngineWeight), ("sh_gate", EngineWeight), ("sh_up", EngineWeight),
+                ("sh_down", EngineWeight), ("shexp_gate", _P)]
+
+
+ENGINE_SIGNATURES = {
+    "moe_engine_create": (_P, [_P, _I]),
+    "moe_engine_destroy": (None, [_P]),
+    "moe_engine_ffn": (_I, [_P, _P, _P, _P, _P, _P, _F, _I, _P, _P, _P, _P, _P]),
+}
+
+
+def load_engine(path=ENGINE_PATH):
+    """The engine-side caller library (built with the library by `make -C rocm-hip_amd`); no GPU call."""
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built: run `make -C rocm-hip_amd` (or __graft_entry__.build())")
+    load_library()  # its dependency, with signatures declared
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in ENGINE_SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
 def gpu_moe_max_tiles(T, n_used, n_expert, tile):
     """include/gpu_ops.h's inline gpu_moe_max_tiles."""
     n = T * n_used

@@ -12,14 +12,19 @@ import moe_hip
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared_functions():
+ENGINE_HEADER = "moe_ffn_engine.h"  # declares the engine-side caller's library (libmoe_ffn_engine.so)
+
+
+def declared_functions(engine=False):
     names = set()
     for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        if (os.path.basename(h) == ENGINE_HEADER) != engine:
+            continue
         src = open(h).read()
         src = re.sub(r"//[^\n]*", "", src)
         src = re.sub(r"static inline[^{]*\{.*?\n\}", "", src, flags=re.S)  # header-only helpers
         for m in re.finditer(r"^(?:const\s+)?(?:hipError_t|int|void|size_t|int32_t|int64_t|uint8_t|uint32_t|uint64_t|float|char|"
-                             r"gguf_model_t)\s*\**\s*(\w+)\s*\(", src, flags=re.M):
+                             r"gguf_model_t|moe_engine)\s*\**\s*(\w+)\s*\(", src, flags=re.M):
             names.add(m.group(1))
     return names
 
@@ -40,6 +45,21 @@ def test_library_exports_every_declared_symbol():
 def test_binding_covers_every_declared_symbol():
     assert declared_functions() <= set(moe_hip.SIGNATURES), declared_functions() - set(moe_hip.SIGNATURES)
     moe_hip.load_library()  # declares every signature without touching the GPU
+
+
+def test_engine_library_exports_its_header():
+    """libmoe_ffn_engine.so exports (C linkage) every function include/moe_ffn_engine.h declares, and the binding
+    declares them; it needs only the library's symbols and the HIP runtime's."""
+    names = declared_functions(engine=True)
+    assert names == set(moe_hip.ENGINE_SIGNATURES), names ^ set(moe_hip.ENGINE_SIGNATURES)
+    out = subprocess.run(["nm", "-D", "--defined-only", moe_hip.ENGINE_PATH], capture_output=True, text=True).stdout
+    assert names <= {line.split()[-1] for line in out.splitlines() if " T " in line}
+    moe_hip.load_engine()
+    und = subprocess.run(["nm", "-D", "--undefined-only", moe_hip.ENGINE_PATH], capture_output=True, text=True).stdout
+    lib = ctypes.CDLL(moe_hip.LIB_PATH)
+    missing = [ln.split()[-1] for ln in und.splitlines()
+               if " U " in ln and "@" not in ln and not hasattr(lib, ln.split()[-1])]
+    assert not missing, missing
 
 
 def test_exports_are_c_linkage():
