@@ -23,6 +23,9 @@
 #include "moe_layer.h"
 #include "qmatvec.h"
 
+#ifndef FD_SHARED_NO_ROUTE
+#define FD_SHARED_NO_ROUTE 1  // the shared expert's units skip the routing (config 1: 18.75 -> 18.59 us per layer)
+#endif
 #ifndef FD_GU_RW
 #define FD_GU_RW 4              // gate / up rows per wave in kernel 2 (64 / FD_GU_RW waves per workgroup)
 #endif
@@ -120,7 +123,12 @@ __global__ void __launch_bounds__(64 * (64 / FD_GU_RW)) k_fd_gate_up(FArgs a) {
     const int FE = a.FE, NU = a.NU, nbf = FE / 32;
     const int slot = blockIdx.x / nbf, b = blockIdx.x - slot * nbf;
     stamp(a, 2);
+#if FD_SHARED_NO_ROUTE
+    // the shared expert's units need no routing: their loads start at once (workgroup 0, a routed unit, publishes)
+    if (slot < NU) router_select(a.logits_in ? a.logits_in : a.logits, a.NE, NU, s_ids, s_wts);
+#else
     router_select(a.logits_in ? a.logits_in : a.logits, a.NE, NU, s_ids, s_wts);
+#endif
     if (blockIdx.x == 0 && tid < NU) {  // the routing for kernel 3 and the caller
         a.ids[tid] = s_ids[tid];
         a.wts[tid] = s_wts[tid];
