@@ -91,6 +91,51 @@ __device__ __forceinline__ float rms_first_pass(const float* xr, const float* ar
     return 1.0f / sqrtf(tot / (float)n + eps);
 }
 
+// Whether a row (and its addend) can take rms_first_pass4: n % 4 == 0, 16-byte aligned
+__device__ __forceinline__ bool rms_rows4(const float* xr, const float* ar, int n) {
+    return (n & 3) == 0 && (((uintptr_t)xr | (uintptr_t)(ar ? ar : xr)) & 15) == 0;
+}
+
+// The first pass for rows that rms_rows4 admits (n <= 4096): thread t's values 4 t + 1024 k + j (k < 4, j < 4) --
+// the layout of the F32 row dot's 16-byte loads (f32_row_dot), so that a router-row dot can use them in place --
+// loaded as 16-byte pieces (every load unconditional, past the end the last piece, unused), into keep; returns the
+// row's 1 / sqrt(mean(v^2) + eps), the squares summed in (k, j) order per thread, then over the workgroup. The
+// producer kernel (gpu_add_rmsnorm) and the fused layer share it, so they give the same bits.
+__device__ __forceinline__ float rms_first_pass4(const float* xr, const float* ar, int n, float eps, float4 (&keep)[4],
+                                                 float* part) {
+    const int t = threadIdx.x, n4 = n >> 2;
+    float4 xv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xv[k] = ((const float4*)xr)[min(t + 256 * k, n4 - 1)];
+    if (ar) {
+        float4 av[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) av[k] = ((const float4*)ar)[min(t + 256 * k, n4 - 1)];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const bool in = t + 256 * k < n4;
+            keep[k] = in ? make_float4(xv[k].x + av[k].x, xv[k].y + av[k].y, xv[k].z + av[k].z, xv[k].w + av[k].w)
+                         : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) keep[k] = t + 256 * k < n4 ? xv[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        ss += keep[k].x * keep[k].x;
+        ss += keep[k].y * keep[k].y;
+        ss += keep[k].z * keep[k].z;
+        ss += keep[k].w * keep[k].w;
+    }
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) part[t >> 6] = ss;
+    __syncthreads();
+    const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+    return 1.0f / sqrtf(tot / (float)n + eps);
+}
+
 // Timestamp k of this workgroup (the 100 MHz wall clock), when stamps are requested: kernel 1 uses slots 0, 1,
 // kernel 2 slots 2..4 and 7, kernel 3 slots 5, 6 of row blockIdx.x of a [max grid][8] table
 __device__ __forceinline__ void stamp(const FArgs& a, int k) {
@@ -168,6 +213,28 @@ __device__ __forceinline__ void quantize_row_q8_0(const float* x, int E, int8_t*
                                             (q[4] & 0xff) | ((q[5] & 0xff) << 8) | ((q[6] & 0xff) << 16) |
                                                 ((uint32_t)q[7] << 24));
             if ((tid & 3) == 0) xd[i0 / 32] = __half2float(__float2half(am / 127.0f));
+        }
+    }
+}
+
+// The same Q8_0 blocks from values in rms_first_pass4's layout (thread t's float4 k: values 4 (t + 256 k) ..): a
+// block of 32 is eight lanes; the same expressions as quantize_row_q8_0, so the same bits. E % 32 == 0.
+__device__ __forceinline__ void quantize_row4_q8_0(const float4 (&y4)[4], int E, int8_t* xq, float* xd) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int c = tid + 256 * k;  // this thread's 16-byte piece
+        if (256 * k >= E / 4) break;  // (uniform)
+        const bool in = c < E / 4;
+        const float4 v = in ? y4[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float am = fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(v.x)), fabsf(v.y)), fabsf(v.z)), fabsf(v.w));
+        am = group_max<8>(am);
+        const float id = am != 0.0f ? 127.0f / am : 0.0f;
+        if (in) {
+            const int q0 = (int)rintf(v.x * id), q1 = (int)rintf(v.y * id), q2 = (int)rintf(v.z * id),
+                      q3 = (int)rintf(v.w * id);
+            *(uint32_t*)(xq + 4 * c) = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((uint32_t)q3 << 24);
+            if ((tid & 7) == 0) xd[c / 8] = __half2float(__float2half(am / 127.0f));
         }
     }
 }

@@ -44,13 +44,85 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
     // the dot takes f32_row_dot's order (16-byte loads, lane i, i + 256, ... of the row) and sums
     const float* wrow = a.w_router + (size_t)blockIdx.x * E;
     const bool pre = a.norm && (int)blockIdx.x < a.NE && (E & 3) == 0 && ((uintptr_t)wrow & 15) == 0;
+    // the shared expert's gate workgroup with the norm: its gate vector loaded the same way
+    const bool gate_wg = (int)blockIdx.x == a.NE + (a.xo.qK ? E / 256 : 1);
+    const bool pre_gate = a.norm && gate_wg && a.w_shexp && (E & 3) == 0 && ((uintptr_t)a.w_shexp & 15) == 0;
     float4 wpre[FD_MAX_E / 1024];
-    if (pre)
+    if (pre || pre_gate)
 #pragma unroll
         for (int k = 0; k < FD_MAX_E / 1024; ++k)
-            if (tid + 256 * k < E / 4) wpre[k] = ((const float4*)wrow)[tid + 256 * k];
-    if (a.norm) {  // every workgroup forms the normalized input itself (E <= 4096 values, from L2)
-        float wn[16];  // the norm weights, loaded with x and add (under a per-value branch they had waited in turn)
+            if (tid + 256 * k < E / 4) wpre[k] = ((const float4*)(pre ? wrow : a.w_shexp))[tid + 256 * k];
+    if (a.norm && rms_rows4(a.x, a.add, E)) {
+        // every workgroup forms the normalized input itself (E <= 4096 values, from L2) in the 16-byte layout of the
+        // router-row dot (rms_first_pass4): a router workgroup dots it in place, with f32_row_dot's order; the
+        // others stage it in LDS
+        float4 wn4[4];  // the norm weights, loaded with x and add (16-byte pieces when the weights are aligned)
+        const bool wa = ((uintptr_t)a.w_norm & 15) == 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int c = min(tid + 256 * k, E / 4 - 1);
+            if (!a.w_norm)
+                wn4[k] = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+            else if (wa)
+                wn4[k] = ((const float4*)a.w_norm)[c];
+            else
+                wn4[k] = make_float4(a.w_norm[4 * c], a.w_norm[4 * c + 1], a.w_norm[4 * c + 2], a.w_norm[4 * c + 3]);
+        }
+        float4 keep4[4];
+        const float inv = rms_first_pass4(a.x, a.add, E, a.eps, keep4, part);
+#ifdef FD_NORM_STAMPS
+        stamp(a, 3);
+#endif
+        float4 y4[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            y4[k] = make_float4(keep4[k].x * inv * wn4[k].x, keep4[k].y * inv * wn4[k].y, keep4[k].z * inv * wn4[k].z,
+                                keep4[k].w * inv * wn4[k].w);
+        if (blockIdx.x == 0 && a.add && a.x_out)  // workgroup 0 writes the residual
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (tid + 256 * k < E / 4) ((float4*)a.x_out)[tid + 256 * k] = keep4[k];
+        if (pre) {  // a router row: f32_row_dot's expressions on the values in registers
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < FD_MAX_E / 1024; ++k)
+                if (tid + 256 * k < E / 4) {
+                    const float4 w4 = wpre[k], b = y4[k];
+                    acc = fmaf(w4.x, b.x, acc);
+                    acc = fmaf(w4.y, b.y, acc);
+                    acc = fmaf(w4.z, b.z, acc);
+                    acc = fmaf(w4.w, b.w, acc);
+                }
+            const float y = block256_sum(acc, part);
+            if (tid == 0) a.logits[blockIdx.x] = y;
+            stamp(a, 1);
+            return;
+        }
+        if (pre_gate) {  // the shared expert's gate: shexp_gate's expressions on the values in registers
+            float d = 0.0f;
+#pragma unroll
+            for (int k = 0; k < FD_MAX_E / 1024; ++k)
+                if (tid + 256 * k < E / 4) {
+                    const float4 p = y4[k], q = wpre[k];
+                    d += p.x * q.x + p.y * q.y + p.z * q.z + p.w * q.w;
+                }
+            d = block256_sum(d, part);
+            if (tid == 0) a.sg[0] = 1.0f / (1.0f + expf(-d));
+            stamp(a, 1);
+            return;
+        }
+        if (!a.xo.qK && !gate_wg && (int)blockIdx.x >= a.NE) {  // x quantized for gate / up, from the registers
+            quantize_row4_q8_0(y4, E, a.xq, a.xd);
+            stamp(a, 1);
+            return;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (tid + 256 * k < E / 4) ((float4*)ys)[tid + 256 * k] = y4[k];
+        __syncthreads();
+        xv = ys;
+    } else if (a.norm) {  // rows the 16-byte layout does not take: the producer kernel's other first pass
+        float wn[16];
 #pragma unroll
         for (int k = 0; k < 16; ++k) wn[k] = a.w_norm ? a.w_norm[min(tid + 256 * k, E - 1)] : 1.0f;
         float keep[16];

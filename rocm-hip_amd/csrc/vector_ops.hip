@@ -143,7 +143,21 @@ __global__ void __launch_bounds__(256) k_add_rmsnorm(const float* x_in, const fl
     const bool kept = n <= 256 * KEEP;
     float inv;
     float wn[KEEP];  // kept rows: the weights, loaded with x and add
-    if (kept) {
+    if (kept && rms_rows4(xr, ar, n)) {
+        // the squares in the 16-byte layout (rms_first_pass4, shared with the fused layer), then the values moved
+        // through LDS into this kernel's layout (t + 256 k: one per thread and 256-value block for the quantizer)
+        __shared__ __align__(16) float row4[256 * KEEP];
+#pragma unroll
+        for (int k = 0; k < KEEP; ++k) wn[k] = w ? w[min(t + 256 * k, n - 1)] : 1.0f;
+        float4 keep4[4];
+        inv = rms_first_pass4(xr, ar, n, eps, keep4, part);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (t + 256 * k < n / 4) ((float4*)row4)[t + 256 * k] = keep4[k];
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < KEEP; ++k) keep[k] = t + 256 * k < n ? row4[t + 256 * k] : 0.0f;
+    } else if (kept) {
 #pragma unroll
         for (int k = 0; k < KEEP; ++k) wn[k] = w ? w[min(t + 256 * k, n - 1)] : 1.0f;
         inv = rms_first_pass(xr, ar, n, eps, keep, part);
