@@ -383,16 +383,15 @@ namespace {
 #define FD_Q8K_RS 4
 #endif
 
-// Q4_K kernel 3 over a.T rows of workgroups: k_fd_down_q8k when FE is its size, else the SwiGLU kernel and k_fd_down
+// Q4_K kernel 3 over a.T rows of workgroups: k_fd_down_q8k. fused_shape_ok admits Q4_K only with down's lane shape
+// 16 x 1 unit of 64 values, i.e. FE == FD_Q8K_FE, and E is a multiple of 256 (every caller has passed
+// moe_fused_prepare); any other shape returns hipErrorInvalidValue rather than run a path no test covers.
 template <int LO, int NO>
 hipError_t launch_down_q8k(const FArgs& a, const qmatvec_q8* qa, hipStream_t st) {
+    (void)qa;
     constexpr int RS = FD_Q8K_RS;  // row sets a workgroup
-    if (a.FE == FD_Q8K_FE && a.E % (RS * (64 / LO)) == 0 && LO * NO * 64 == FD_Q8K_FE)
-        return launch_kernel(k_fd_down_q8k<LO, NO, RS>, dim3(a.E / (RS * (64 / LO)), a.T), dim3(64 * a.NS), 0, st, a);
-    hipError_t e = gpu_swiglu(a.g, a.u, a.act, a.T * a.NS * a.FE, qa, st);
-    if (e == hipSuccess)
-        e = launch_kernel(k_fd_down<QT_Q4_K, LO, NO>, dim3(a.E / (64 / LO), a.T), dim3(64 * a.NS), 0, st, a);
-    return e;
+    if (a.FE != FD_Q8K_FE || a.E % (RS * (64 / LO)) != 0 || LO * NO * 64 != FD_Q8K_FE) return hipErrorInvalidValue;
+    return launch_kernel(k_fd_down_q8k<LO, NO, RS>, dim3(a.E / (RS * (64 / LO)), a.T), dim3(64 * a.NS), 0, st, a);
 }
 
 // kernels: bit 0, 1, 2 launch kernel 1, 2 (with Q4_K's SwiGLU), 3 (7 in normal use; a subset only for profiling)
