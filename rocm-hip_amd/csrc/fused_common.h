@@ -51,6 +51,9 @@ struct FArgs {
     float eps;
     int norm;
     int T, E, NE, NU, FE, NS, has_gate, ids_ld;
+    // T = 1 (set by the launcher): kernel 2 routes by rank counting over the whole workgroup and publishes only the
+    // ids; kernel 3 has one more wave that forms the renormalised weights from the logits
+    int rank_route;
 };
 
 // The RMSNorm producer fused into the layer (moe_layer_forward_norm): its arguments

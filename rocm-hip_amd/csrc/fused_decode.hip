@@ -5,11 +5,14 @@
 // Here the layer is three launches with no grid-wide synchronisation inside any of them:
 //   1  one workgroup per router-logit row, one that quantizes x (the activation quantizer's expressions) and
 //      one for the shared-expert gate;
-//   2  one workgroup per (slot, 32-row block of FE): it routes (the router's own code on the logits, every
-//      workgroup for itself; workgroup 0 also publishes ids / weights), then computes the slot expert's 32 gate
-//      and 32 up rows, SwiGLU, and the Q8_0 quantization of those 32 values (one Q8_0 block of down's input);
+//   2  one workgroup per (slot, 32-row block of FE): it routes (every workgroup for itself; workgroup 0 also
+//      publishes the ids), then computes the slot expert's 32 gate and 32 up rows, SwiGLU, and the Q8_0
+//      quantization of those 32 values (one Q8_0 block of down's input). The top-k is a rank count over the
+//      whole workgroup (router_rank_select: the router's ids, in its order, in two LDS passes where the router's
+//      one-wave selection takes nu rounds of wave reductions: -0.85 us on the critical path at 128 experts);
 //   3  one workgroup per 64 / L output rows (L: the down row dot's lanes), one wave per slot: their down rows,
-//      then the combine in slot order.
+//      then the combine in slot order; one more wave forms the renormalised weights from the logits and the ids
+//      (the router's expressions) while the slots' rows load.
 // Every sum is formed in the same order as the per-operation kernels (rows_dot's lane groups and DPP group sums,
 // the same router, quantizer and combine), so the layer's output equals the per-operation path bit for bit.
 // (A single persistent kernel with two grid barriers was measured slower: each barrier's cross-XCD fences and
@@ -70,9 +73,6 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
         }
         float4 keep4[4];
         const float inv = rms_first_pass4(a.x, a.add, E, a.eps, keep4, part);
-#ifdef FD_NORM_STAMPS
-        stamp(a, 3);
-#endif
         float4 y4[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k)
@@ -190,22 +190,35 @@ __global__ void __launch_bounds__(64 * (64 / FD_GU_RW)) k_fd_gate_up(FArgs a) {
     static_assert(R >= 1, "a wave's rows must cover its lane groups");
     __shared__ int s_ids[65];
     __shared__ float s_wts[64];
+    __shared__ __align__(16) uint64_t s_pk[256];
+    __shared__ __align__(16) uint64_t s_pk2[256];
     __shared__ float gu[2][32];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, gl = lane & (L_IN - 1), grp = lane / L_IN;
     const int FE = a.FE, NU = a.NU, nbf = FE / 32;
     const int slot = blockIdx.x / nbf, b = blockIdx.x - slot * nbf;
     stamp(a, 2);
+    const float* lg = a.logits_in ? a.logits_in : a.logits;
 #if FD_SHARED_NO_ROUTE
     // the shared expert's units need no routing: their loads start at once (workgroup 0, a routed unit, publishes)
-    if (slot < NU) router_select(a.logits_in ? a.logits_in : a.logits, a.NE, NU, s_ids, s_wts);
+    if (slot < NU) {
+        if (a.rank_route)  // (uniform) every thread counts ranks; kernel 3 forms the weights
+            router_rank_select<64 * (64 / FD_GU_RW)>(lg, a.NE, NU, s_ids, s_pk, s_pk2);
+        else
+            router_select(lg, a.NE, NU, s_ids, s_wts);
+    }
 #else
-    router_select(a.logits_in ? a.logits_in : a.logits, a.NE, NU, s_ids, s_wts);
+    if (a.rank_route)
+        router_rank_select<64 * (64 / FD_GU_RW)>(lg, a.NE, NU, s_ids, s_pk, s_pk2);
+    else
+        router_select(lg, a.NE, NU, s_ids, s_wts);
 #endif
     if (blockIdx.x == 0 && tid < NU) {  // the routing for kernel 3 and the caller
         a.ids[tid] = s_ids[tid];
-        a.wts[tid] = s_wts[tid];
         if (a.ids_out) a.ids_out[tid] = s_ids[tid];
-        if (a.wts_out) a.wts_out[tid] = s_wts[tid];
+        if (!a.rank_route) {
+            a.wts[tid] = s_wts[tid];
+            if (a.wts_out) a.wts_out[tid] = s_wts[tid];
+        }
     }
     stamp(a, 3);
     const int e = slot < NU ? s_ids[slot] : -1;
@@ -245,26 +258,33 @@ template <int TYPE, int L_OUT, int NUPL_OUT>
 __global__ void __launch_bounds__(1024) k_fd_down(FArgs a) {
     constexpr int RB = 64 / L_OUT;
     __shared__ float downv[16][RB];
+    __shared__ float s_wts[64];
     const int tid = threadIdx.x, E = a.E, FE = a.FE, NU = a.NU, NS = a.NS, t = blockIdx.y;
     const int slot = tid >> 6, lane = tid & 63, gl = lane & (L_OUT - 1), i = lane / L_OUT;
     const int i0 = blockIdx.x * RB;
     stamp(a, 5);
-    const int e = slot < NU ? a.ids[t * a.ids_ld + slot] : -1;
-    const long long row = e >= 0 ? (long long)e * E + i0 + i : i0 + i;
-    const int mi = e >= 0 ? 2 : 5;
-    const uint8_t* vr[1] = {pick(a.v, mi) + row * a.vrb_out};
-    const uint8_t* sr[1] = {pick(a.s, mi) + row * a.srb_out};
-    constexpr bool Q8K = Fmt<TYPE>::Q8K;
-    const long long sl = (long long)t * NS + slot;  // this (token, slot) pair's row of down's input
-    const int8_t* xq[1] = {Q8K ? a.aqk + sl * FE : a.act_q + sl * FE};
-    const float* xd[1] = {Q8K ? a.adk + sl * (FE / 256) : a.act_d + sl * (FE / 32)};
-    const int* xbs[1] = {Q8K ? a.absk + sl * (FE / 16) : nullptr};
-    float acc[1];
-    rows_dot_multi<TYPE, L_OUT, 1, NUPL_OUT>(vr, sr, xq, xd, xbs, fmt_units(TYPE, FE), gl, 1, acc);
-    if (gl == 0) downv[slot][i] = acc[0];
+    if (slot < NS) {
+        const int e = slot < NU ? a.ids[t * a.ids_ld + slot] : -1;
+        const long long row = e >= 0 ? (long long)e * E + i0 + i : i0 + i;
+        const int mi = e >= 0 ? 2 : 5;
+        const uint8_t* vr[1] = {pick(a.v, mi) + row * a.vrb_out};
+        const uint8_t* sr[1] = {pick(a.s, mi) + row * a.srb_out};
+        constexpr bool Q8K = Fmt<TYPE>::Q8K;
+        const long long sl = (long long)t * NS + slot;  // this (token, slot) pair's row of down's input
+        const int8_t* xq[1] = {Q8K ? a.aqk + sl * FE : a.act_q + sl * FE};
+        const float* xd[1] = {Q8K ? a.adk + sl * (FE / 256) : a.act_d + sl * (FE / 32)};
+        const int* xbs[1] = {Q8K ? a.absk + sl * (FE / 16) : nullptr};
+        float acc[1];
+        rows_dot_multi<TYPE, L_OUT, 1, NUPL_OUT>(vr, sr, xq, xd, xbs, fmt_units(TYPE, FE), gl, 1, acc);
+        if (gl == 0) downv[slot][i] = acc[0];
+    } else {  // (rank_route: the wave after the slots) the renormalised weights, while the slots' rows load
+        const float* lg = (a.logits_in ? a.logits_in : a.logits) + (size_t)t * a.NE;
+        router_weights_one_wave(lg, a.NE, NU, a.ids + t * a.ids_ld, s_wts);
+        if (blockIdx.x == 0 && a.wts_out && lane < NU) a.wts_out[t * NU + lane] = s_wts[lane];
+    }
     __syncthreads();
     if (tid < RB) {  // the combine kernel's expression
-        const float* wts = a.wts + t * NU;
+        const float* wts = a.rank_route ? s_wts : a.wts + t * NU;
         float o = wts[0] * downv[0][tid];
         for (int j = 1; j < NU; ++j) o += wts[j] * downv[j][tid];
         if (NS > NU) o += a.has_gate ? downv[NU][tid] * a.sg[t] : downv[NU][tid];
@@ -274,8 +294,8 @@ __global__ void __launch_bounds__(1024) k_fd_down(FArgs a) {
 }
 
 // ---- kernel 3 for Q4_K, token blockIdx.y (T = 1, or up to 4 tokens after the per-operation id launch of gate / up):
-// down's Q8_K input formed here instead of by a SwiGLU launch before it. Each slot's wave reads its slot's fp32 gate / up rows (FE = 1024: 16 consecutive values a lane, 16 lanes per
-// 256-value block), forms SiLU(g) u (the SwiGLU kernel's expression) and the Q8_K blocks (the quantizer's: the
+// down's Q8_K input formed here instead of by a SwiGLU launch before it. Each slot's wave reads its slot's fp32
+// gate / up rows (FE = 1024: 16 consecutive values a lane, 16 lanes per 256-value block), forms SiLU(g) u (the SwiGLU kernel's expression) and the Q8_K blocks (the quantizer's: the
 // signed value of largest |x| with the lowest index on ties, iscale = -127 / it, q = min(127, rint(iscale x)),
 // d = 1 / iscale, sums of 16), into its own LDS; its weight loads are issued first. Then RS sets of 64 / L_OUT
 // output rows with the per-operation down shape (L_OUT lanes, NUPL_OUT units a lane), and the combine in slot order.
@@ -291,80 +311,87 @@ __global__ void __launch_bounds__(1024) k_fd_down_q8k(FArgs a) {
     __shared__ __align__(16) int8_t aq[16][FD_Q8K_FE];
     __shared__ float adk[16][FD_Q8K_FE / 256];
     __shared__ __align__(16) int abk[16][FD_Q8K_FE / 16];
+    __shared__ float s_wts[64];
     const int tid = threadIdx.x, E = a.E, FE = a.FE, NU = a.NU, NS = a.NS, t = blockIdx.y;
     const int slot = tid >> 6, lane = tid & 63, gl = lane & (L_OUT - 1), i = lane / L_OUT;
     const int i0 = blockIdx.x * RB * RS;
     const long long sl = (long long)t * NS + slot;  // this (token, slot) pair's gate / up row
     stamp(a, 5);
-    const int e = slot < NU ? a.ids[t * a.ids_ld + slot] : -1;
-    const int mi = e >= 0 ? 2 : 5;
-    const long long rbase = e >= 0 ? (long long)e * E : 0;
-    const uint8_t* vb = pick(a.v, mi) + rbase * a.vrb_out;
-    const uint8_t* sb = pick(a.s, mi) + rbase * a.srb_out;
-    const int nu_out = fmt_units(QT_Q4_K, FE);
-    WUnit<QT_Q4_K> wu[RS][NUPL_OUT];
+    if (slot < NS) {
+        const int e = slot < NU ? a.ids[t * a.ids_ld + slot] : -1;
+        const int mi = e >= 0 ? 2 : 5;
+        const long long rbase = e >= 0 ? (long long)e * E : 0;
+        const uint8_t* vb = pick(a.v, mi) + rbase * a.vrb_out;
+        const uint8_t* sb = pick(a.s, mi) + rbase * a.srb_out;
+        const int nu_out = fmt_units(QT_Q4_K, FE);
+        WUnit<QT_Q4_K> wu[RS][NUPL_OUT];
 #pragma unroll
-    for (int r = 0; r < RS; ++r) {
-        const long long row = i0 + RB * r + i;
+        for (int r = 0; r < RS; ++r) {
+            const long long row = i0 + RB * r + i;
 #pragma unroll
-        for (int c = 0; c < NUPL_OUT; ++c)
-            load_packed<QT_Q4_K>(vb + row * a.vrb_out, sb + row * a.srb_out, gl + c * L_OUT, nu_out, wu[r][c]);
-    }
-    {  // this slot's SwiGLU and Q8_K blocks
-        const float4* g4 = (const float4*)(a.g + sl * FE + 16 * lane);
-        const float4* u4 = (const float4*)(a.u + sl * FE + 16 * lane);
-        float v[16];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float4 g = g4[k], u = u4[k];
-            const float gg[4] = {g.x, g.y, g.z, g.w}, uu[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) v[4 * k + j] = gg[j] / (1.0f + __expf(-gg[j])) * uu[j];
+            for (int c = 0; c < NUPL_OUT; ++c)
+                load_packed<QT_Q4_K>(vb + row * a.vrb_out, sb + row * a.srb_out, gl + c * L_OUT, nu_out, wu[r][c]);
         }
-        float ba = fabsf(v[0]), bv = v[0];
-        int bi = 16 * (lane & 15);  // index within the 256-value block
+        {  // this slot's SwiGLU and Q8_K blocks
+            const float4* g4 = (const float4*)(a.g + sl * FE + 16 * lane);
+            const float4* u4 = (const float4*)(a.u + sl * FE + 16 * lane);
+            float v[16];
 #pragma unroll
-        for (int k = 1; k < 16; ++k)
-            if (fabsf(v[k]) > ba) {
-                ba = fabsf(v[k]);
-                bv = v[k];
-                bi = 16 * (lane & 15) + k;
+            for (int k = 0; k < 4; ++k) {
+                const float4 g = g4[k], u = u4[k];
+                const float gg[4] = {g.x, g.y, g.z, g.w}, uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[4 * k + j] = gg[j] / (1.0f + __expf(-gg[j])) * uu[j];
             }
-        argmax_step<1>(ba, bv, bi);
-        argmax_step<2>(ba, bv, bi);
-        argmax_step<4>(ba, bv, bi);
-        argmax_step<8>(ba, bv, bi);
-        const float iscale = ba != 0.0f ? -127.0f / bv : 0.0f;
-        int q[16], s16 = 0;
+            float ba = fabsf(v[0]), bv = v[0];
+            int bi = 16 * (lane & 15);  // index within the 256-value block
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            q[k] = ba != 0.0f ? min(127, (int)rintf(iscale * v[k])) : 0;
-            s16 += q[k];
+            for (int k = 1; k < 16; ++k)
+                if (fabsf(v[k]) > ba) {
+                    ba = fabsf(v[k]);
+                    bv = v[k];
+                    bi = 16 * (lane & 15) + k;
+                }
+            argmax_step<1>(ba, bv, bi);
+            argmax_step<2>(ba, bv, bi);
+            argmax_step<4>(ba, bv, bi);
+            argmax_step<8>(ba, bv, bi);
+            const float iscale = ba != 0.0f ? -127.0f / bv : 0.0f;
+            int q[16], s16 = 0;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                q[k] = ba != 0.0f ? min(127, (int)rintf(iscale * v[k])) : 0;
+                s16 += q[k];
+            }
+            uint32_t pk[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                pk[k] = (q[4 * k] & 0xff) | ((q[4 * k + 1] & 0xff) << 8) | ((q[4 * k + 2] & 0xff) << 16) |
+                        ((uint32_t)q[4 * k + 3] << 24);
+            *(uint4*)&aq[slot][16 * lane] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+            if ((lane & 15) == 0) adk[slot][lane >> 4] = ba != 0.0f ? 1.0f / iscale : 0.0f;
+            abk[slot][lane] = s16;
         }
-        uint32_t pk[4];
+        // (the slot's own wave reads what it wrote: LDS operations of a wave complete in order)
+        XUnit<QT_Q4_K> x[NUPL_OUT];
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-            pk[k] = (q[4 * k] & 0xff) | ((q[4 * k + 1] & 0xff) << 8) | ((q[4 * k + 2] & 0xff) << 16) |
-                    ((uint32_t)q[4 * k + 3] << 24);
-        *(uint4*)&aq[slot][16 * lane] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        if ((lane & 15) == 0) adk[slot][lane >> 4] = ba != 0.0f ? 1.0f / iscale : 0.0f;
-        abk[slot][lane] = s16;
-    }
-    // (the slot's own wave reads what it wrote: LDS operations of a wave complete in order)
-    XUnit<QT_Q4_K> x[NUPL_OUT];
+        for (int c = 0; c < NUPL_OUT; ++c) load_x<QT_Q4_K>(aq[slot], adk[slot], abk[slot], gl + c * L_OUT, x[c]);
 #pragma unroll
-    for (int c = 0; c < NUPL_OUT; ++c) load_x<QT_Q4_K>(aq[slot], adk[slot], abk[slot], gl + c * L_OUT, x[c]);
+        for (int r = 0; r < RS; ++r) {
+            float acc = 0.0f;
 #pragma unroll
-    for (int r = 0; r < RS; ++r) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NUPL_OUT; ++c) acc += term<QT_Q4_K>(wu[r][c], x[c], gl + c * L_OUT);
-        acc = group_sum<L_OUT>(acc);
-        if (gl == 0) downv[slot][RB * r + i] = acc;
+            for (int c = 0; c < NUPL_OUT; ++c) acc += term<QT_Q4_K>(wu[r][c], x[c], gl + c * L_OUT);
+            acc = group_sum<L_OUT>(acc);
+            if (gl == 0) downv[slot][RB * r + i] = acc;
+        }
+    } else {  // (rank_route: the wave after the slots) the renormalised weights, while the slots' rows load
+        const float* lg = (a.logits_in ? a.logits_in : a.logits) + (size_t)t * a.NE;
+        router_weights_one_wave(lg, a.NE, NU, a.ids + t * a.ids_ld, s_wts);
+        if (blockIdx.x == 0 && a.wts_out && lane < NU) a.wts_out[t * NU + lane] = s_wts[lane];
     }
     __syncthreads();
     if (tid < RB * RS) {  // the combine kernel's expression
-        const float* wts = a.wts + t * NU;
+        const float* wts = a.rank_route ? s_wts : a.wts + t * NU;
         float o = wts[0] * downv[0][tid];
         for (int j = 1; j < NU; ++j) o += wts[j] * downv[j][tid];
         if (NS > NU) o += a.has_gate ? downv[NU][tid] * a.sg[t] : downv[NU][tid];
@@ -391,7 +418,8 @@ hipError_t launch_down_q8k(const FArgs& a, const qmatvec_q8* qa, hipStream_t st)
     (void)qa;
     constexpr int RS = FD_Q8K_RS;  // row sets a workgroup
     if (a.FE != FD_Q8K_FE || a.E % (RS * (64 / LO)) != 0 || LO * NO * 64 != FD_Q8K_FE) return hipErrorInvalidValue;
-    return launch_kernel(k_fd_down_q8k<LO, NO, RS>, dim3(a.E / (RS * (64 / LO)), a.T), dim3(64 * a.NS), 0, st, a);
+    return launch_kernel(k_fd_down_q8k<LO, NO, RS>, dim3(a.E / (RS * (64 / LO)), a.T),
+                         dim3(64 * (a.NS + a.rank_route)), 0, st, a);
 }
 
 // kernels: bit 0, 1, 2 launch kernel 1, 2 (with Q4_K's SwiGLU), 3 (7 in normal use; a subset only for profiling)
@@ -408,7 +436,8 @@ hipError_t launch_fused(const FArgs& a, const qmatvec_q8* qa, int kernels, hipSt
         return e;
     }
     if (e == hipSuccess && (kernels & 4))
-        e = launch_kernel(k_fd_down<TYPE, LO, NO>, dim3(a.E / (64 / LO)), dim3(64 * a.NS), 0, st, a);
+        e = launch_kernel(k_fd_down<TYPE, LO, NO>, dim3(a.E / (64 / LO)), dim3(64 * (a.NS + a.rank_route)), 0, st,
+                          a);
     return e;
 }
 
@@ -616,6 +645,9 @@ bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits,
     a.out = out;
     a.ids_out = ids_out;
     a.wts_out = wts_out;
+    // Top-k by rank counting in kernel 2, the weights in an extra wave of kernel 3 (s_pk holds 256 keys; the
+    // extra wave needs a 17th wave of room)
+    a.rank_route = a.NE <= 256 && a.NS < 16 ? 1 : 0;
     *err = moe_fused_launch(d, a, scratch, kernels, st);
     return true;
 }

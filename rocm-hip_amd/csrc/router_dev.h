@@ -134,6 +134,28 @@ __device__ __forceinline__ uint32_t wave_min_u32_uniform(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
+// The softmax's normalisation on one wave: lane l's logits l, l + 64, ... (NPL of them; -inf past ne) into v, the
+// maximum mx and 1 / (sum of exp(logit - mx)), the sum in lane order and then over the wave (the router's bits)
+template <int NPL>
+__device__ __forceinline__ void router_softmax_norm(const float* lg, int ne, float (&v)[NPL], float& mx, float& inv) {
+    const int lane = threadIdx.x & 63;
+    mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) v[j] = lg[min(lane + 64 * j, ne - 1)];  // (all loads in flight at once)
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+        if (lane + 64 * j >= ne) v[j] = -INFINITY;
+        mx = fmaxf(mx, v[j]);
+    }
+    mx = wave_max(mx);
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j)
+        if (lane + 64 * j < ne) sum += expf(v[j] - mx);
+    sum = wave_sum(sum);
+    inv = 1.0f / sum;
+}
+
 // Selection on one wave; lane l holds logits l, l + 64, ... (NPL of them) as order keys (0: taken or absent, below
 // every real key; -0 is keyed as +0). Each of the nu rounds takes the largest remaining key (a max reduction), then
 // the lowest index holding it (a min reduction), so ties go to the lower index. Lane r keeps round r's logit and
@@ -143,23 +165,13 @@ __device__ __forceinline__ void router_select_wave(const float* lg, int ne, int 
     const int lane = threadIdx.x & 63;
     float v[NPL];
     uint32_t key[NPL];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < NPL; ++j) v[j] = lg[min(lane + 64 * j, ne - 1)];  // (all loads in flight at once)
+    float mx, inv;
+    router_softmax_norm<NPL>(lg, ne, v, mx, inv);
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
         const int e = lane + 64 * j;
-        if (e >= ne) v[j] = -INFINITY;
         key[j] = e < ne ? f32_order_key(v[j] == 0.0f ? 0.0f : v[j]) : 0u;
-        mx = fmaxf(mx, v[j]);
     }
-    mx = wave_max(mx);
-    float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NPL; ++j)
-        if (lane + 64 * j < ne) sum += expf(v[j] - mx);
-    sum = wave_sum(sum);
-    const float inv = 1.0f / sum;
     uint32_t mykey = 0;
     int myid = 0;
     for (int r = 0; r < nu; ++r) {
@@ -207,6 +219,104 @@ __device__ __forceinline__ void router_select_one_wave(const float* lg, int ne, 
 __device__ __forceinline__ void router_select(const float* lg, int ne, int nu, int* id_row, float* wts) {
     if (threadIdx.x < 64) router_select_one_wave(lg, ne, nu, id_row, wts);
     __syncthreads();
+}
+
+// The nu selected experts by rank, by a whole workgroup of NT threads (up to 256 experts). Keys: 64 bits, the order
+// key of the logit, then nep - 1 - index (all distinct; nep the power of two >= max(ne, 32); padding keys 0), so the
+// selection order (larger logit; on equal logits the lower index) is the keys' descending order. A key's rank is the
+// number of larger keys, counted by G threads (two keys a read). Two stages, to keep the LDS reads few: the rank of
+// every key within its group of 32, then, over the nu' = min(nu, 32) best of each group (which hold the nu best
+// overall), the rank among those. The same ids, in the same order, as router_select (nu rounds of reductions on
+// one wave). s_ids[0..nu) on return (visible to the workgroup); s_pk, s_pk2: 256 8-byte words of LDS each,
+// 16-byte aligned.
+template <int G>
+__device__ __forceinline__ int keys_above(const uint64_t* seg, int per, uint64_t pc) {
+    int cnt = 0;
+    for (int j = 0; j < per; j += 2) {
+        const ulonglong2 q = *(const ulonglong2*)(seg + j);
+        cnt += q.x > pc ? 1 : 0;
+        cnt += q.y > pc ? 1 : 0;
+    }
+    return group_sum_i<G>(cnt);
+}
+
+// Stage 1, G threads a key: rank within the key's group of 32; the nu' best of group k go to s_pk2[k nu' + rank]
+template <int G>
+__device__ __forceinline__ void rank_in_groups(const uint64_t* s_pk, int nep, int nu1, uint64_t* s_pk2) {
+    const int tid = threadIdx.x, c = tid / G, g = tid - c * G, cc = min(c, nep - 1);  // (no early exit: DPP sums)
+    const uint64_t pc = s_pk[cc];
+    const int r = keys_above<G>(s_pk + (cc & ~31) + g * (32 / G), 32 / G, pc);
+    if (g == 0 && c < nep && r < nu1) s_pk2[(c >> 5) * nu1 + r] = pc;
+}
+
+// Stage 2, G threads a key of s_pk2[0..n2) (n2p: a power of two >= n2, zero-padded): the rank among them
+template <int G>
+__device__ __forceinline__ void rank_survivors(const uint64_t* s_pk2, int n2, int n2p, int nep, int ne, int nu,
+                                               int* s_ids) {
+    const int tid = threadIdx.x, c = tid / G, g = tid - c * G;
+    const uint64_t pc = s_pk2[min(c, n2 - 1)];
+    const int r = keys_above<G>(s_pk2 + g * (n2p / G), n2p / G, pc);
+    const int idx = nep - 1 - (int)(uint32_t)pc;
+    if (g == 0 && c < n2 && r < nu && idx < ne) s_ids[r] = idx;
+}
+
+template <int NT>
+__device__ __forceinline__ void router_rank_select(const float* lg, int ne, int nu, int* s_ids, uint64_t* s_pk,
+                                                   uint64_t* s_pk2) {
+    static_assert(NT >= 4 * 256, "at least 4 threads for each of up to 256 keys");
+    const int tid = threadIdx.x;
+    int nep = 32;
+    while (nep < ne) nep <<= 1;
+    const int nu1 = min(nu, 32), n2 = (nep >> 5) * nu1;
+    int n2p = 32;
+    while (n2p < n2) n2p <<= 1;
+    for (int i = tid; i < nep; i += NT) {
+        const float v = lg[min(i, ne - 1)];
+        const uint32_t key = i < ne ? f32_order_key(v == 0.0f ? 0.0f : v) : 0u;
+        s_pk[i] = (uint64_t)key << 32 | (uint32_t)(nep - 1 - i);
+    }
+    for (int i = n2 + tid; i < n2p; i += NT) s_pk2[i] = 0;  // (disjoint from stage 1's writes)
+    __syncthreads();
+    // G threads a key, each over 32 / G keys two at a time: G <= 16
+    switch (min(NT / nep, 16)) {  // (uniform)
+    case 16: rank_in_groups<16>(s_pk, nep, nu1, s_pk2); break;
+    case 8: rank_in_groups<8>(s_pk, nep, nu1, s_pk2); break;
+    default: rank_in_groups<4>(s_pk, nep, nu1, s_pk2); break;
+    }
+    __syncthreads();
+    switch (min(NT / n2p, 16)) {  // (uniform) n2p / G >= 2
+    case 16: rank_survivors<16>(s_pk2, n2, n2p, nep, ne, nu, s_ids); break;
+    case 8: rank_survivors<8>(s_pk2, n2, n2p, nep, ne, nu, s_ids); break;
+    default: rank_survivors<4>(s_pk2, n2, n2p, nep, ne, nu, s_ids); break;
+    }
+    __syncthreads();
+}
+
+// The renormalised weights of the selected experts ids[0..nu) (selection order) on one wave, with router_select's
+// expressions: p = exp(logit - mx) / sum over every expert, then p / max(sum of the selected p in rank order,
+// 6.103515625e-5). Lanes < nu write wts[lane].
+__device__ __forceinline__ void router_weights_one_wave(const float* lg, int ne, int nu, const int* ids, float* wts) {
+    const int lane = threadIdx.x & 63;
+    float mx, inv;
+    if (ne <= 128) {
+        float v[2];
+        router_softmax_norm<2>(lg, ne, v, mx, inv);
+    } else if (ne <= 256) {
+        float v[4];
+        router_softmax_norm<4>(lg, ne, v, mx, inv);
+    } else if (ne <= 512) {
+        float v[8];
+        router_softmax_norm<8>(lg, ne, v, mx, inv);
+    } else {
+        float v[16];
+        router_softmax_norm<16>(lg, ne, v, mx, inv);
+    }
+    const float l = lane < nu ? lg[ids[lane]] : 0.0f;
+    const float p = expf((l == 0.0f ? 0.0f : l) - mx) * inv;
+    float ws = 0.0f;
+    for (int r = 0; r < nu; ++r) ws += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), r));  // rank order
+    ws = fmaxf(ws, 6.103515625e-5f);
+    if (lane < nu) wts[lane] = p / ws;
 }
 
 #endif  // ROUTER_DEV_H
