@@ -263,6 +263,7 @@ __global__ void __launch_bounds__(1024) k_fd_down(FArgs a) {
     const int slot = tid >> 6, lane = tid & 63, gl = lane & (L_OUT - 1), i = lane / L_OUT;
     const int i0 = blockIdx.x * RB;
     stamp(a, 5);
+    const float sgv = a.has_gate && tid < RB ? a.sg[t] : 0.0f;  // (read now: kernel 1 wrote it)
     if (slot < NS) {
         const int e = slot < NU ? a.ids[t * a.ids_ld + slot] : -1;
         const long long row = e >= 0 ? (long long)e * E + i0 + i : i0 + i;
@@ -287,7 +288,7 @@ __global__ void __launch_bounds__(1024) k_fd_down(FArgs a) {
         const float* wts = a.rank_route ? s_wts : a.wts + t * NU;
         float o = wts[0] * downv[0][tid];
         for (int j = 1; j < NU; ++j) o += wts[j] * downv[j][tid];
-        if (NS > NU) o += a.has_gate ? downv[NU][tid] * a.sg[t] : downv[NU][tid];
+        if (NS > NU) o += a.has_gate ? downv[NU][tid] * sgv : downv[NU][tid];
         a.out[(size_t)t * E + i0 + tid] = o;
     }
     stamp(a, 6);
@@ -317,6 +318,7 @@ __global__ void __launch_bounds__(1024) k_fd_down_q8k(FArgs a) {
     const int i0 = blockIdx.x * RB * RS;
     const long long sl = (long long)t * NS + slot;  // this (token, slot) pair's gate / up row
     stamp(a, 5);
+    const float sgv = a.has_gate && tid < RB * RS ? a.sg[t] : 0.0f;  // (read now: kernel 1 wrote it)
     if (slot < NS) {
         const int e = slot < NU ? a.ids[t * a.ids_ld + slot] : -1;
         const int mi = e >= 0 ? 2 : 5;
@@ -394,7 +396,7 @@ __global__ void __launch_bounds__(1024) k_fd_down_q8k(FArgs a) {
         const float* wts = a.rank_route ? s_wts : a.wts + t * NU;
         float o = wts[0] * downv[0][tid];
         for (int j = 1; j < NU; ++j) o += wts[j] * downv[j][tid];
-        if (NS > NU) o += a.has_gate ? downv[NU][tid] * a.sg[t] : downv[NU][tid];
+        if (NS > NU) o += a.has_gate ? downv[NU][tid] * sgv : downv[NU][tid];
         a.out[(long long)t * E + i0 + tid] = o;
     }
     stamp(a, 6);

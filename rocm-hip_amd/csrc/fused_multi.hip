@@ -361,6 +361,7 @@ __global__ void __launch_bounds__(1024) k_fm_down(FArgs a) {
     const int T = a.T, E = a.E, FE = a.FE, NU = a.NU, NS = a.NS;
     const int gl = lane & (L_OUT - 1), i = lane / L_OUT, i0 = blockIdx.x * RB, nu_out = fmt_units(TYPE, FE);
     stamp(a, 5);
+    const float sgv = a.has_gate && tid < T * RB ? a.sg[tid / RB] : 0.0f;  // (read now: kernel 1 wrote it)
     const int nitems = T * NS;
     if (tid < nitems) {  // item tid: token tid / NS, slot tid % NS (slot NU: the shared expert)
         const int t = tid / NS, j = tid - t * NS;
@@ -410,7 +411,7 @@ __global__ void __launch_bounds__(1024) k_fm_down(FArgs a) {
         const int t = tid / RB, r = tid - t * RB;
         float o = s_wts[t][0] * downv[t][0][r];
         for (int j = 1; j < NU; ++j) o += s_wts[t][j] * downv[t][j][r];
-        if (NS > NU) o += a.has_gate ? downv[t][NU][r] * a.sg[t] : downv[t][NU][r];
+        if (NS > NU) o += a.has_gate ? downv[t][NU][r] * sgv : downv[t][NU][r];
         a.out[(size_t)t * E + i0 + r] = o;
     }
     stamp(a, 6);
