@@ -139,9 +139,10 @@ hipError_t qmatvec_launch_q8_id_batch(int type, const void *W, size_t row_bytes,
 // (rows native rows of row_size(type, K) bytes, device memory) and builds its split-plane copy on the stream:
 // per row, the value bytes of every block in one plane and the scale bytes in another, so that each lane
 // streams 16-byte loads. The launchers above then read the copy for any W inside the registered range. The
-// caller keeps W unchanged while registered; qmatvec_unpack_weights(W) frees the copy. Q8_0 / ROCmFP4 / FAST
+// caller keeps W unchanged while registered; qmatvec_unpack_weights(W) frees the copy. Q8_0 / ROCmFP4 / FAST / Q4_K
 // matrices of whole 32-row groups (K % 256 == 0) also get the prefill MFMA kernels' operand tiles (Q8_0: the
-// native size; the FP4 types: ~1.56 times it). Device memory per registered matrix: native + planes + tiles.
+// native size; the FP4 types: ~1.56 times it; Q4_K ~1.67 times). Device memory per registered matrix: native +
+// planes + tiles.
 hipError_t qmatvec_pack_weights(int type, const void *W, size_t row_bytes, long long rows, int K, hipStream_t stream);
 // The same with flags (0: as qmatvec_pack_weights):
 //   QMATVEC_PACK_INPLACE: the split planes replace the native rows in W itself (no copy: every launcher reads the
@@ -149,8 +150,8 @@ hipError_t qmatvec_pack_weights(int type, const void *W, size_t row_bytes, long 
 //     returns hipErrorInvalidValue). The call waits for the rewrite (it uses a transient buffer of the matrix's
 //     size); qmatvec_unpack_weights(W) writes the native rows back before it returns.
 //   QMATVEC_PACK_NO_TILES: no operand tiles (prefill then runs the per-entry kernels on the planes).
-// Device memory held per matrix, W included: default 3x native for Q8_0 (3.56x FP4); INPLACE 2x (2.56x);
-// INPLACE | NO_TILES 1x.
+// Device memory held per matrix, W included: default 3x native for Q8_0 (3.56x FP4, 3.67x Q4_K); INPLACE 2x
+// (2.56x, 2.67x); INPLACE | NO_TILES 1x.
 #define QMATVEC_PACK_INPLACE 1
 #define QMATVEC_PACK_NO_TILES 2
 hipError_t qmatvec_pack_weights_ex(int type, void *W, size_t row_bytes, long long rows, int K, int flags,

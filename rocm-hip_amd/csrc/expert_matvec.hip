@@ -174,8 +174,10 @@ __global__ void __launch_bounds__(256) k_pack(const uint8_t* W, long long row_by
 //   Q8_0:      16-byte slots: the block's int8 values 16 h .. 16 h + 15 (the int8 MFMA's A);
 //   FP4 types: 12-byte slots: the block's values 8 h .. 8 h + 7, then 16 + 8 h .. + 7 (the f16 MFMAs' A of each
 //              16-value half), each as the FP6 E2M3 code of codebook value / 2, 6 bits per value from bit 0 up.
-// Scale tiles, per group g and 8-block group q, 32 row slots: Q8_0 16 bytes (8 blocks' FP16 d); FP4 types 32 bytes
-// (per block the FP16 pair (e0, e1) of its UE4M3 half-scales, FAST (e, e)).
+//   Q4_K:      the same 12-byte slots per 32-value sub-block, each code the FP6 E2M3 of quant / 2 (quant 0..15).
+// Scale tiles, per group g and 8-block group q (Q4_K: super-block), 32 row slots: Q8_0 16 bytes (8 blocks' FP16 d);
+// FP4 types 32 bytes (per block the FP16 pair (e0, e1) of its UE4M3 half-scales, FAST (e, e)); Q4_K 48 bytes (the
+// sub-block scales sc0..sc7 as FP16, the mins m0..m7 as FP16, then the FP16 d and dmin and 12 zero bytes).
 __device__ __forceinline__ uint32_t fp4_code(const uint8_t* qs, int v) {  // code of value v (0..31) of a block
     return v < 16 ? (qs[v] & 0x0fu) : (qs[v - 16] >> 4);
 }
@@ -184,6 +186,18 @@ __device__ __forceinline__ uint32_t fp4_code(const uint8_t* qs, int v) {  // cod
 __device__ __forceinline__ uint32_t fp4_to_e2m3(uint32_t c) {
     const uint8_t tab[8] = {0x00, 0x04, 0x08, 0x0c, 0x10, 0x14, 0x18, 0x1a};
     return tab[c & 7] | ((c & 8) << 2);  // E2M3 sign is bit 5
+}
+// The E2M3 code of q / 2 for a Q4_K quant q (0..15): 0, 0.5 (subnormal 4/8), then (1 + m / 8) 2^(e - 1):
+// 1, 1.5 (e 1), 2, 2.5, 3, 3.5 (e 2), 4, 4.5, .., 7.5 (e 3)
+__device__ __forceinline__ uint32_t q4_to_e2m3(uint32_t q) {
+    const uint8_t tab[16] = {0, 4, 8, 12, 16, 18, 20, 22, 24, 25, 26, 27, 28, 29, 30, 31};
+    return tab[q & 15];
+}
+// Value v (0..255) of a Q4_K super-block: the low nibble of byte 32 c + l of the quants for v = 64 c + l (l < 32),
+// the high nibble for v = 64 c + 32 + l
+__device__ __forceinline__ uint32_t q4k_quant(const uint8_t* blk, int v) {
+    const uint8_t b = blk[16 + 32 * (v >> 6) + (v & 31)];
+    return (v & 32) ? (b >> 4) : (b & 15u);
 }
 
 template <int TYPE>
@@ -198,7 +212,8 @@ __global__ void __launch_bounds__(256) k_pack_tiles(const uint8_t* W, long long 
         const int l = (int)(i & 63), h = l >> 5;
         const long long gb = i >> 6, g = gb / nb;
         const int b = (int)(gb - g * nb);
-        const uint8_t* blk = W + (32 * g + (l & 31)) * row_bytes + (long long)b * BB;
+        // the native block holding block b (Q4_K: super-block b / 8, of which b is sub-block b % 8)
+        const uint8_t* blk = W + (32 * g + (l & 31)) * row_bytes + (long long)(TYPE == QT_Q4_K ? b >> 3 : b) * BB;
         uint8_t* dst = V + SS * i;
         if constexpr (TYPE == QT_Q8_0) {
             for (int j = 0; j < 16; ++j) dst[j] = blk[2 + 16 * h + j];
@@ -206,7 +221,11 @@ __global__ void __launch_bounds__(256) k_pack_tiles(const uint8_t* W, long long 
             uint32_t w[3] = {0u, 0u, 0u};
             for (int n = 0; n < 16; ++n) {
                 const int v = (n < 8 ? 8 * h : 16 + 8 * h) + (n & 7);
-                const uint32_t f = fp4_to_e2m3(fp4_code(blk, v));
+                uint32_t f;
+                if constexpr (TYPE == QT_Q4_K)
+                    f = q4_to_e2m3(q4k_quant(blk, 32 * (b & 7) + v));
+                else
+                    f = fp4_to_e2m3(fp4_code(blk, v));
                 const int bit = 6 * n;
                 w[bit >> 5] |= f << (bit & 31);
                 if ((bit & 31) > 26) w[(bit >> 5) + 1] |= f >> (32 - (bit & 31));
@@ -221,8 +240,26 @@ __global__ void __launch_bounds__(256) k_pack_tiles(const uint8_t* W, long long 
     const long long r = k / nq;
     const int q = (int)(k - r * nq);
     const uint8_t* row = W + r * row_bytes;
-    constexpr int SB = TYPE == QT_Q8_0 ? 16 : 32;  // slot bytes
+    constexpr int SB = TYPE == QT_Q8_0 ? 16 : TYPE == QT_Q4_K ? Q4K_TILE_SLOT : 32;  // slot bytes
     uint8_t* dst = S + ((r / 32) * nq + q) * (32 * SB) + (r & 31) * SB;
+    if constexpr (TYPE == QT_Q4_K) {  // super-block q: sc0..sc7, m0..m7 as FP16 (exact: 6-bit integers), d, dmin
+        const uint8_t* blk = row + (long long)q * BB;
+        uint32_t sw[3];
+        for (int j = 0; j < 3; ++j)
+            sw[j] = (uint32_t)blk[4 + 4 * j] | (uint32_t)blk[5 + 4 * j] << 8 | (uint32_t)blk[6 + 4 * j] << 16 |
+                    (uint32_t)blk[7 + 4 * j] << 24;
+        uint16_t* o = (uint16_t*)dst;
+        for (int j = 0; j < 8; ++j) {
+            int sc, mn;
+            q4k_scale_min(j, sw, sc, mn);
+            o[j] = __half_as_ushort(__float2half((float)sc));
+            o[8 + j] = __half_as_ushort(__float2half((float)mn));
+        }
+        o[16] = (uint16_t)(blk[0] | blk[1] << 8);  // d
+        o[17] = (uint16_t)(blk[2] | blk[3] << 8);  // dmin
+        for (int j = 18; j < 24; ++j) o[j] = 0;
+        return;
+    }
     for (int b = 0; b < 8; ++b) {
         const uint8_t* blk = row + (long long)(8 * q + b) * BB;
         if constexpr (TYPE == QT_Q8_0) {
@@ -252,7 +289,8 @@ struct Packed {
 // Whether a registered matrix also gets MFMA operand tiles: a type of the MFMA kernels, whole 32-row groups and
 // whole 8-block scale groups
 bool tiles_ok(int type, long long rows, int K) {
-    return (type == QT_Q8_0 || type == QT_ROCMFP4 || type == QT_ROCMFP4_FAST) && rows % 32 == 0 && K % 256 == 0;
+    return (type == QT_Q8_0 || type == QT_ROCMFP4 || type == QT_ROCMFP4_FAST || type == QT_Q4_K) && rows % 32 == 0 &&
+           K % 256 == 0;
 }
 
 std::mutex g_pack_mu;
@@ -455,13 +493,11 @@ static hipError_t launch_pack(const void* W, size_t rb, long long rows, int K, u
     uint8_t* V = mem;
     uint8_t* S = mem + (size_t)rows * fmt_value_row(TYPE, K);
     hipError_t e = hipSuccess;
-    if constexpr (TYPE != QT_Q4_K) {  // the tiles first: an in-place registration overwrites W after them
-        if (tiles) {
-            const long long nt = rows / 32 * (K / 32) * 64 + rows * (K / 256);
-            e = launch_kernel(k_pack_tiles<TYPE>, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st,
-                              (const uint8_t*)W, (long long)rb, rows, K, tiles,
-                              tiles + (size_t)rows * tile_value_row(TYPE, K));  // scale tiles after the values
-        }
+    if (tiles) {  // the tiles first: an in-place registration overwrites W after them
+        const long long nt = rows / 32 * (K / 32) * 64 + rows * (K / 256);
+        e = launch_kernel(k_pack_tiles<TYPE>, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st,
+                          (const uint8_t*)W, (long long)rb, rows, K, tiles,
+                          tiles + (size_t)rows * tile_value_row(TYPE, K));  // scale tiles after the values
     }
     if (e == hipSuccess)
         e = launch_kernel(k_pack<TYPE, false>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
@@ -483,7 +519,7 @@ static hipError_t pack_type(int type, const void* W, size_t rb, long long rows, 
     case QT_Q8_0: return launch_pack<QT_Q8_0>(W, rb, rows, K, planes, tiles, st);
     case QT_ROCMFP4: return launch_pack<QT_ROCMFP4>(W, rb, rows, K, planes, tiles, st);
     case QT_ROCMFP4_FAST: return launch_pack<QT_ROCMFP4_FAST>(W, rb, rows, K, planes, tiles, st);
-    default: return launch_pack<QT_Q4_K>(W, rb, rows, K, planes, nullptr, st);
+    default: return launch_pack<QT_Q4_K>(W, rb, rows, K, planes, tiles, st);
     }
 }
 

@@ -43,12 +43,16 @@ struct Fmt<QT_Q4_K> {
 
 __host__ __device__ constexpr int fmt_value_row(int type, int K) { return type == QT_Q8_0 ? K : K / 2; }
 __host__ __device__ constexpr int fmt_scale_row(int type, int K) { return type == QT_ROCMFP4_FAST ? K / 32 : K / 16; }
-// Bytes per row in the MFMA operand tiles. Values: Q8_0 its int8 values; the FP4 types their codes re-encoded as
-// FP6 E2M3 (6 bits each: every codebook value / 2 is exact in E2M3, which the hardware decodes 32 at a time).
-// Scales: Q8_0 its FP16 d (2 per block); the FP4 types each block's (e0, e1) UE4M3 half-scales decoded to an FP16
-// pair (FAST: (e, e)), 4 per block
+// Bytes per row in the MFMA operand tiles. Values: Q8_0 its int8 values; the FP4 types and Q4_K their codes
+// re-encoded as FP6 E2M3 (6 bits each: every codebook value / 2, and every 4-bit Q4_K quant / 2, is exact in E2M3,
+// which the hardware decodes 32 at a time). Scales: Q8_0 its FP16 d (2 per block); the FP4 types each block's
+// (e0, e1) UE4M3 half-scales decoded to an FP16 pair (FAST: (e, e)), 4 per block; Q4_K per super-block of 256 a
+// 48-byte slot: the eight 6-bit sub-block scales and the eight mins as FP16, then d and dmin (Q4K_TILE_SLOT)
+#define Q4K_TILE_SLOT 48
 __host__ __device__ constexpr int tile_value_row(int type, int K) { return type == QT_Q8_0 ? K : K / 4 * 3; }
-__host__ __device__ constexpr int tile_scale_row(int type, int K) { return type == QT_Q8_0 ? K / 16 : K / 8; }
+__host__ __device__ constexpr int tile_scale_row(int type, int K) {
+    return type == QT_Q8_0 ? K / 16 : type == QT_Q4_K ? K / 256 * Q4K_TILE_SLOT : K / 8;
+}
 __host__ __device__ constexpr int fmt_units(int type, int K) { return type == QT_Q4_K ? K / 64 : K / 32; }
 
 template <int TYPE>

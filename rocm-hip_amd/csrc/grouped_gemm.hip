@@ -77,6 +77,7 @@ struct GArgs {
     const uint8_t* ss2;
     int kr, sT;
     long long sout;
+    const int* xbs;  // Q4_K: the Q8_K activations' sums of 16 values, rows of K / 16 (xq / xd: Q8_K values / scales)
 };
 #define GX_IN 1
 #define GX_OUT 2
@@ -149,9 +150,20 @@ struct HBuf {  // FP4 types
     uint8_t b[KB][GG_NT][2][1024];   // [block][entry tile][16-value half][lane * 16]: FP16 activations
     float dx[KB / 4][GG_TILE][4];
 };
+template <int NM, int KB>
+struct KBuf {  // Q4_K: one stage = one 128-value half of a super-block (KB == 4 sub-blocks)
+    uint8_t a[NM][4][KB][1024];      // [matrix][wave][sub-block][lane * 16]: 12-byte FP6 slots
+    uint8_t b[KB][GG_NT][2][1024];   // [sub-block][entry tile][16-value half][lane * 16]: FP16 activations
+    _Float16 bs[GG_TILE][8];         // [entry][16-value sum of the stage]: Q8_K sums of 16 as FP16
+    float dx[GG_TILE];               // [entry]: the Q8_K scale of the stage's super-block
+};
 template <int TYPE, int NM, int KB>
 struct BufOf {
     typedef GBuf<TYPE, NM, KB> type;
+};
+template <int NM, int KB>
+struct BufOf<QT_Q4_K, NM, KB> {
+    typedef KBuf<NM, KB> type;
 };
 template <int NM, int KB>
 struct BufOf<QT_ROCMFP4, NM, KB> {
@@ -276,8 +288,8 @@ __device__ __forceinline__ void h_issue(HBuf<NM, KB>& B, int b0, uint4 (&wsc)[NM
 
 // This thread's activation units, converted, into the FP16 operand runs: values 0..7 of a unit to the slot of
 // (entry, K half 0) of its MFMA half, values 8..15 to that of (entry, K half 1)
-template <int NM, int KB>
-__device__ __forceinline__ void h_stage_b(HBuf<NM, KB>& B, const uint4 (&xb)[KB / 2], int tid) {
+template <int NM, int KB, typename Buf = HBuf<NM, KB>>
+__device__ __forceinline__ void h_stage_b(Buf& B, const uint4 (&xb)[KB / 2], int tid) {
     const int e = tid & 63, h = (tid >> 6) & 1;
 #pragma unroll
     for (int j = 0; j < KB / 2; ++j) {
@@ -320,6 +332,106 @@ __device__ __forceinline__ void h_compute(const HBuf<NM, KB>& B, const uint4 (&w
             }
         }
         __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// ------------------------------------------------------------------ Q4_K: exact f16 MFMA, integer sums per 128 values
+//
+// Per 128-value half c of a super-block (one stage of four 32-value sub-blocks j), for each (row, entry):
+//   isum = sum_j sc_j . sum_{i in j} q_i qx_i   on eight f16 MFMAs with A = sc_j q (the FP6 codes decoded with the
+//          factor 2, times the FP16 sub-block scale: integers <= 945, exact), B = qx (Q8_K values, exact): every
+//          partial sum an integer below 945 x 127 x 128 < 2^24, so exact in fp32 in any order;
+//   msum = sum_j m_j (bs_2j + bs_2j+1)         on one 32 x 32 x 8 f16 MFMA (mins <= 63, sums of 16 <= 2032: exact);
+//   acc += dx (d isum - dmin msum)            d, dmin per row (FP16, broadcast by an outer-product MFMA), dx the
+//                                              entry's Q8_K scale: three VALU operations per output and 128 values.
+// The reference's K-quant WMMA kernel forms the same integer sums per 128-value chunk (src/matvec_q.hip:2952-3008)
+// and the same float step.
+struct KSc {  // a lane's row scales for the stage: sc_4c..sc_4c+3 and m_4c..m_4c+3 as FP16, (d, dmin)
+    uint2 sc, m;
+    uint32_t dd;
+};
+
+template <int NM, int KB>
+__device__ __forceinline__ void k_issue(KBuf<NM, KB>& B, int b0, KSc& ks, const uint8_t* vt, const uint8_t* sct,
+                                        const int8_t* xu, int xs, uint4 (&xb)[KB / 2], int4& bsv, float& dxv,
+                                        const int* bsr, const float* dxr, int w, int tid) {
+    static_assert(KB == 4, "a Q4_K stage is one 128-value half of a super-block");
+#pragma unroll
+    for (int c = 0; c < KB; ++c) lds_load12(vt + 768 * (b0 + c), B.a[0][w][c]);
+#pragma unroll
+    for (int j = 0; j < KB / 2; ++j) xb[j] = *(const uint4*)(xu + xs * (b0 + (tid >> 7) + 2 * j));
+    if (tid < 128) bsv = *(const int4*)(bsr + 2 * b0);  // entry tid % 64, sums 4 (tid / 64) .. + 3 of the stage
+    else if (tid < 192) dxv = dxr[b0 >> 3];             // entry tid - 128
+    const uint8_t* slot = sct + Q4K_TILE_SLOT * 32 * (b0 >> 3);
+    const int c = (b0 >> 2) & 1;
+    ks.sc = *(const uint2*)(slot + 8 * c);
+    ks.m = *(const uint2*)(slot + 16 + 8 * c);
+    ks.dd = *(const uint32_t*)(slot + 32);
+}
+
+template <int NM, int KB>
+__device__ __forceinline__ void k_stage(KBuf<NM, KB>& B, const uint4 (&xb)[KB / 2], const int4& bsv, float dxv,
+                                        int tid) {
+    h_stage_b<NM, KB>(B, xb, tid);
+    if (tid < 128) {
+        const h2 lo = {(_Float16)bsv.x, (_Float16)bsv.y}, hi = {(_Float16)bsv.z, (_Float16)bsv.w};  // exact
+        *(uint2*)&B.bs[tid & 63][4 * (tid >> 6)] = make_uint2(__builtin_bit_cast(uint32_t, lo),
+                                                               __builtin_bit_cast(uint32_t, hi));
+    } else if (tid < 192) {
+        B.dx[tid - 128] = dxv;
+    }
+}
+
+template <int NM, int KB, int NTU>
+__device__ __forceinline__ void k_compute(const KBuf<NM, KB>& B, const KSc& ks, v16f (&acc)[NM][NTU], int w, int l,
+                                          int lr, int kh) {
+    const v16f z = {};
+    // D[j] = d, Dm[j] = dmin of the lane's row 8 (j / 4) + 4 kh + j % 4: outer products with ones (exact)
+    const _Float16 one = kh ? (_Float16)0.0f : (_Float16)1.0f;
+    const h2 dd = __builtin_bit_cast(h2, ks.dd);
+    const v4h ad = {kh ? (_Float16)0.0f : dd.x, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+    const v4h adm = {kh ? (_Float16)0.0f : dd.y, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+    const v4h b1 = {one, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+    const v16f D = __builtin_amdgcn_mfma_f32_32x32x8f16(ad, b1, z, 0, 0, 0);
+    const v16f Dm = __builtin_amdgcn_mfma_f32_32x32x8f16(adm, b1, z, 0, 0, 0);
+    // A of the four sub-blocks: codes decoded two sub-blocks at a time, times the sub-block's scale
+    v8h A0[KB], A1[KB];
+#pragma unroll
+    for (int bp = 0; bp < KB; bp += 2) {
+        const uint3 c0 = *(const uint3*)(B.a[0][w][bp] + 16 * l);
+        const uint3 c1 = *(const uint3*)(B.a[0][w][bp + 1] + 16 * l);
+        const v32h d = __builtin_amdgcn_cvt_scalef32_pk32_f16_fp6((v6u){c0.x, c0.y, c0.z, c1.x, c1.y, c1.z}, 2.0f);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int jj = bp + kk;
+            const uint32_t scw = jj < 2 ? ks.sc.x : ks.sc.y;
+            const uint32_t sc = __builtin_amdgcn_perm(scw, scw, (jj & 1) ? 0x03020302u : 0x01000100u);  // (sc, sc)
+            A0[jj] = scaled8(d, 2 * kk, sc);
+            A1[jj] = scaled8(d, 2 * kk + 1, sc);
+        }
+    }
+    // M's A: k = 4 kh .. 4 kh + 3 hold m of sub-blocks 2 kh, 2 kh, 2 kh + 1, 2 kh + 1 (each against a sum of 16)
+    const uint32_t mw = kh ? ks.m.y : ks.m.x;
+    const v4h Am = __builtin_bit_cast(v4h, make_uint2(__builtin_amdgcn_perm(mw, mw, 0x01000100u),
+                                                       __builtin_amdgcn_perm(mw, mw, 0x03020302u)));
+#pragma unroll
+    for (int t = 0; t < NTU; ++t) {
+        v16f P = z;
+#pragma unroll
+        for (int jj = 0; jj < KB; ++jj) {
+            const v8h B0 = *(const v8h*)(B.b[jj][t][0] + 16 * l);
+            const v8h B1 = *(const v8h*)(B.b[jj][t][1] + 16 * l);
+            P = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                A1[jj], B1, __builtin_amdgcn_mfma_f32_32x32x16_f16(A0[jj], B0, P, 0, 0, 0), 0, 0, 0);
+        }
+        const v4h Bm = *(const v4h*)&B.bs[32 * t + lr][4 * kh];
+        const v16f M = __builtin_amdgcn_mfma_f32_32x32x8f16(Am, Bm, z, 0, 0, 0);
+        const float dxv = B.dx[32 * t + lr];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const float mm = Dm[j] * M[j];
+            acc[0][t][j] = fmaf(fmaf(D[j], P[j], -mm), dxv, acc[0][t][j]);
+        }
     }
 }
 
@@ -396,7 +508,8 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
     // this lane's slots in its value and scale tiles (scale slots: 16 bytes per 8 blocks for Q8_0, 32 for FP4)
     const int r0 = rb * GG_ROWS + 32 * w;
     const long long grp = ((long long)e * a.N + r0) / 32;
-    constexpr int SB = F16 ? 32 : 16;
+    constexpr bool Q4K = TYPE == QT_Q4_K;
+    constexpr int SB = Q4K ? Q4K_TILE_SLOT : F16 ? 32 : 16;
     constexpr int VS = F16 ? 12 : 16;  // value slot bytes
     const uint8_t* vt[NM];
     const uint8_t* sct[NM];
@@ -415,7 +528,27 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
 #pragma unroll
         for (int t = 0; t < NTU; ++t) acc[m][t] = (v16f){};
     const int nst = nb / KB;
-    if constexpr (!F16) {
+    if constexpr (Q4K) {
+        static_assert(NM == 1, "Q4_K: one matrix a launch (down's Q8_K input is quantized per 256 values)");
+        const int ue = tid & 63, uh = (tid >> 6) & 1;
+        const int8_t* xu = a.xq + (long long)in_row(min(ue, cnt - 1)) * K + 16 * uh;
+        // the entry whose sums of 16 (threads 0..127) or scale (threads 128..191) this thread stages
+        const long long br = in_row(min(tid & 63, cnt - 1));
+        const int* bsr = a.xbs + br * (K / 16) + 4 * ((tid >> 6) & 1);
+        const float* kdr = a.xd + (long long)in_row(min((tid - 128) & 63, cnt - 1)) * (K / 256);
+        KSc ks;
+        uint4 xb[KB / 2];
+        int4 bsv = {};
+        float dxv = 0.0f;
+        for (int s = 0; s < nst; ++s) {
+            k_issue<NM, KB>(buf, s * KB, ks, vt[0], sct[0], xu, 32, xb, bsv, dxv, bsr, kdr, w, tid);
+            wait_vm<0>();
+            k_stage<NM, KB>(buf, xb, bsv, dxv, tid);
+            __syncthreads();
+            k_compute<NM, KB, NTU>(buf, ks, acc, w, l, lr, kh);
+            __syncthreads();
+        }
+    } else if constexpr (!F16) {
         // this lane's activation run: entry 32 (w % GG_NT) + lr, K half kh
         const int8_t* xrow;
         int xs;  // bytes from one block's run to the next
@@ -502,8 +635,8 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
 // Whether the MFMA kernels take this matrix: a split-plane type with Q8_0 activations, whole 128-row blocks and
 // whole K stages (of either kernel)
 bool moe_grouped_mfma_ok(int type, int N, int K) {
-    return (type == QT_Q8_0 || type == QT_ROCMFP4 || type == QT_ROCMFP4_FAST) && N % GG_ROWS == 0 &&
-           K % (GG_KB * 32) == 0 && K % (GG_KB2 * 32) == 0;
+    return (type == QT_Q8_0 || type == QT_ROCMFP4 || type == QT_ROCMFP4_FAST || type == QT_Q4_K) && N % GG_ROWS == 0 &&
+           K % (GG_KB * 32) == 0 && K % (GG_KB2 * 32) == 0 && (type != QT_Q4_K || K % 256 == 0);
 }
 
 // The entry tile the MFMA kernel takes
@@ -522,6 +655,13 @@ static void bind_shared(GArgs& a, const GShared* sh, int max_tiles, int& tiles) 
     tiles += (sh->T + GG_TILE - 1) / GG_TILE;
 }
 
+// Q4_K reads the Q8_K part of the activation bundle: values, scales per 256, sums per 16
+static void bind_q8k(GArgs& a, const qmatvec_q8* q) {
+    a.xq = q->qK;
+    a.xd = q->dK;
+    a.xbs = q->bsK;
+}
+
 // A 1-D grid with a workgroup for every (tile, row block) item that can exist, rounded up to whole XCD rounds
 static dim3 grid_of(int N, int tiles) {
     const long long n = (long long)(N / GG_ROWS) * tiles;
@@ -538,6 +678,11 @@ hipError_t moe_launch_grouped_mfma(int type, const uint8_t* v, const uint8_t* s,
     int tiles = max_tiles;
     bind_shared(a, sh, max_tiles, tiles);
     const dim3 g = grid_of(N, tiles), b(256);
+    if (type == QT_Q4_K) {  // Q8_K activations, rows as they are
+        if (xt || sh) return hipErrorInvalidValue;
+        bind_q8k(a, q);
+        return launch_kernel(k_grouped<QT_Q4_K, 1, GG_KB>, g, b, 0, stream, a);
+    }
     switch (type) {
     case QT_Q8_0: return launch_kernel(k_grouped<QT_Q8_0, 1, GG_KB>, g, b, 0, stream, a);
     case QT_ROCMFP4: return launch_kernel(k_grouped<QT_ROCMFP4, 1, GG_KB>, g, b, 0, stream, a);
@@ -575,7 +720,9 @@ hipError_t moe_launch_dense_mfma(int type, const uint8_t* v, const uint8_t* s, l
     GArgs a = {v,       s,       vrb,     srb,     q->q0, q->d0, y,       N,       K,       nullptr, nullptr,
                nullptr, nullptr, nullptr, nullptr, ldy,   T,     nullptr, nullptr, nullptr, nullptr, 0};
     const dim3 g = grid_of(N, (T + GG_TILE - 1) / GG_TILE), b(256);
+    if (type == QT_Q4_K) bind_q8k(a, q);
     switch (type) {
+    case QT_Q4_K: return launch_kernel(k_grouped<QT_Q4_K, 1, GG_KB>, g, b, 0, stream, a);
     case QT_Q8_0: return launch_kernel(k_grouped<QT_Q8_0, 1, GG_KB>, g, b, 0, stream, a);
     case QT_ROCMFP4: return launch_kernel(k_grouped<QT_ROCMFP4, 1, GG_KB>, g, b, 0, stream, a);
     case QT_ROCMFP4_FAST: return launch_kernel(k_grouped<QT_ROCMFP4_FAST, 1, GG_KB>, g, b, 0, stream, a);

@@ -199,7 +199,9 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
                                    gpu_moe_group_ws_bytes(T, NE), st));
         const uint8_t *vg = nullptr, *sgp = nullptr, *vu = nullptr, *sup = nullptr, *vd = nullptr, *sdp = nullptr;
         long long gvs = 0, gss = 0, dvs = 0, dss = 0;  // tile bytes per 32-row group (gate and up alike, down)
-        if (mode && moe_grouped_mfma_ok(type, FE, E) && moe_grouped_mfma_ok(type, E, FE) &&
+        // (Q4_K: down's input is Q8_K, one scale per 256 values, which a workgroup's 32-row blocks cannot form: its
+        // gate, up, SwiGLU and down run as the separate launches below, each on the MFMA kernel when registered)
+        if (mode && type != 12 && moe_grouped_mfma_ok(type, FE, E) && moe_grouped_mfma_ok(type, E, FE) &&
             moe_packed_tiles(d->w_gate, type, E, rb_in, &vg, &sgp, &gvs, &gss) &&
             moe_packed_tiles(d->w_up, type, E, rb_in, &vu, &sup, &gvs, &gss) &&
             moe_packed_tiles(d->w_down, type, FE, rb_out, &vd, &sdp, &dvs, &dss)) {
