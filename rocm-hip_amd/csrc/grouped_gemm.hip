@@ -151,19 +151,23 @@ struct HBuf {  // FP4 types
     float dx[KB / 4][GG_TILE][4];
 };
 template <int NM, int KB>
-struct KBuf {  // Q4_K: one stage = one 128-value half of a super-block (KB == 4 sub-blocks)
+struct KBuf {  // Q4_K: one stage = one (KB = 4) or two (KB = 8) 128-value halves of a super-block
     uint8_t a[NM][4][KB][1024];      // [matrix][wave][sub-block][lane * 16]: 12-byte FP6 slots
     uint8_t b[KB][GG_NT][2][1024];   // [sub-block][entry tile][16-value half][lane * 16]: FP16 activations
-    _Float16 bs[GG_TILE][8];         // [entry][16-value sum of the stage]: Q8_K sums of 16 as FP16
+    _Float16 bs[GG_TILE][2 * KB];    // [entry][16-value sum of the stage]: Q8_K sums of 16 as FP16
     float dx[GG_TILE];               // [entry]: the Q8_K scale of the stage's super-block
 };
 template <int TYPE, int NM, int KB>
 struct BufOf {
     typedef GBuf<TYPE, NM, KB> type;
 };
+#ifndef GG_KBQ4
+#define GG_KBQ4 4  // Q4_K: 32-value sub-blocks per stage (8, a whole super-block in 68 KB of LDS, measured no faster)
+#endif
+#define KQ GG_KBQ4
 template <int NM, int KB>
 struct BufOf<QT_Q4_K, NM, KB> {
-    typedef KBuf<NM, KB> type;
+    typedef KBuf<NM, KQ> type;
 };
 template <int NM, int KB>
 struct BufOf<QT_ROCMFP4, NM, KB> {
@@ -346,26 +350,35 @@ __device__ __forceinline__ void h_compute(const HBuf<NM, KB>& B, const uint4 (&w
 //                                              entry's Q8_K scale: three VALU operations per output and 128 values.
 // The reference's K-quant WMMA kernel forms the same integer sums per 128-value chunk (src/matvec_q.hip:2952-3008)
 // and the same float step.
-struct KSc {  // a lane's row scales for the stage: sc_4c..sc_4c+3 and m_4c..m_4c+3 as FP16, (d, dmin)
+struct KSc2 {  // a lane's row scales for a 128-value half: sc_4c..sc_4c+3 and m_4c..m_4c+3 as FP16
     uint2 sc, m;
+};
+template <int KB>
+struct KSc {  // ... for a stage of KB / 4 halves, and the super-block's (d, dmin)
+    KSc2 h[KB / 4];
     uint32_t dd;
 };
 
 template <int NM, int KB>
-__device__ __forceinline__ void k_issue(KBuf<NM, KB>& B, int b0, KSc& ks, const uint8_t* vt, const uint8_t* sct,
+__device__ __forceinline__ void k_issue(KBuf<NM, KB>& B, int b0, KSc<KB>& ks, const uint8_t* vt, const uint8_t* sct,
                                         const int8_t* xu, int xs, uint4 (&xb)[KB / 2], int4& bsv, float& dxv,
                                         const int* bsr, const float* dxr, int w, int tid) {
-    static_assert(KB == 4, "a Q4_K stage is one 128-value half of a super-block");
+    static_assert(KB == 4 || KB == 8, "a Q4_K stage is one or two 128-value halves of a super-block");
 #pragma unroll
     for (int c = 0; c < KB; ++c) lds_load12(vt + 768 * (b0 + c), B.a[0][w][c]);
 #pragma unroll
     for (int j = 0; j < KB / 2; ++j) xb[j] = *(const uint4*)(xu + xs * (b0 + (tid >> 7) + 2 * j));
-    if (tid < 128) bsv = *(const int4*)(bsr + 2 * b0);  // entry tid % 64, sums 4 (tid / 64) .. + 3 of the stage
-    else if (tid < 192) dxv = dxr[b0 >> 3];             // entry tid - 128
+    if (tid < 32 * KB) bsv = *(const int4*)(bsr + 2 * b0);  // entry tid % 64, sums 4 (tid / 64) .. + 3 of the stage
+    if (KB == 8 ? tid < 64 : (tid >= 128 && tid < 192)) dxv = dxr[b0 >> 3];  // entry tid % 64
     const uint8_t* slot = sct + Q4K_TILE_SLOT * 32 * (b0 >> 3);
-    const int c = (b0 >> 2) & 1;
-    ks.sc = *(const uint2*)(slot + 8 * c);
-    ks.m = *(const uint2*)(slot + 16 + 8 * c);
+    if constexpr (KB == 8) {
+        const uint4 sc = *(const uint4*)slot, m = *(const uint4*)(slot + 16);
+        ks.h[0] = {make_uint2(sc.x, sc.y), make_uint2(m.x, m.y)};
+        ks.h[1] = {make_uint2(sc.z, sc.w), make_uint2(m.z, m.w)};
+    } else {
+        const int c = (b0 >> 2) & 1;
+        ks.h[0] = {*(const uint2*)(slot + 8 * c), *(const uint2*)(slot + 16 + 8 * c)};
+    }
     ks.dd = *(const uint32_t*)(slot + 32);
 }
 
@@ -373,18 +386,17 @@ template <int NM, int KB>
 __device__ __forceinline__ void k_stage(KBuf<NM, KB>& B, const uint4 (&xb)[KB / 2], const int4& bsv, float dxv,
                                         int tid) {
     h_stage_b<NM, KB>(B, xb, tid);
-    if (tid < 128) {
+    if (tid < 32 * KB) {
         const h2 lo = {(_Float16)bsv.x, (_Float16)bsv.y}, hi = {(_Float16)bsv.z, (_Float16)bsv.w};  // exact
         *(uint2*)&B.bs[tid & 63][4 * (tid >> 6)] = make_uint2(__builtin_bit_cast(uint32_t, lo),
                                                                __builtin_bit_cast(uint32_t, hi));
-    } else if (tid < 192) {
-        B.dx[tid - 128] = dxv;
     }
+    if (KB == 8 ? tid < 64 : (tid >= 128 && tid < 192)) B.dx[tid & 63] = dxv;
 }
 
 template <int NM, int KB, int NTU>
-__device__ __forceinline__ void k_compute(const KBuf<NM, KB>& B, const KSc& ks, v16f (&acc)[NM][NTU], int w, int l,
-                                          int lr, int kh) {
+__device__ __forceinline__ void k_compute(const KBuf<NM, KB>& B, const KSc<KB>& ks, v16f (&acc)[NM][NTU], int w,
+                                          int l, int lr, int kh) {
     const v16f z = {};
     // D[j] = d, Dm[j] = dmin of the lane's row 8 (j / 4) + 4 kh + j % 4: outer products with ones (exact)
     const _Float16 one = kh ? (_Float16)0.0f : (_Float16)1.0f;
@@ -394,43 +406,48 @@ __device__ __forceinline__ void k_compute(const KBuf<NM, KB>& B, const KSc& ks, 
     const v4h b1 = {one, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
     const v16f D = __builtin_amdgcn_mfma_f32_32x32x8f16(ad, b1, z, 0, 0, 0);
     const v16f Dm = __builtin_amdgcn_mfma_f32_32x32x8f16(adm, b1, z, 0, 0, 0);
-    // A of the four sub-blocks: codes decoded two sub-blocks at a time, times the sub-block's scale
-    v8h A0[KB], A1[KB];
 #pragma unroll
-    for (int bp = 0; bp < KB; bp += 2) {
-        const uint3 c0 = *(const uint3*)(B.a[0][w][bp] + 16 * l);
-        const uint3 c1 = *(const uint3*)(B.a[0][w][bp + 1] + 16 * l);
-        const v32h d = __builtin_amdgcn_cvt_scalef32_pk32_f16_fp6((v6u){c0.x, c0.y, c0.z, c1.x, c1.y, c1.z}, 2.0f);
+    for (int hc = 0; hc < KB / 4; ++hc) {  // each 128-value half: its integer sums, then one float step
+        const KSc2& kh2 = ks.h[hc];
+        // A of the half's four sub-blocks: codes decoded two sub-blocks at a time, times the sub-block's scale
+        v8h A0[4], A1[4];
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            const int jj = bp + kk;
-            const uint32_t scw = jj < 2 ? ks.sc.x : ks.sc.y;
-            const uint32_t sc = __builtin_amdgcn_perm(scw, scw, (jj & 1) ? 0x03020302u : 0x01000100u);  // (sc, sc)
-            A0[jj] = scaled8(d, 2 * kk, sc);
-            A1[jj] = scaled8(d, 2 * kk + 1, sc);
+        for (int bp = 0; bp < 4; bp += 2) {
+            const uint3 c0 = *(const uint3*)(B.a[0][w][4 * hc + bp] + 16 * l);
+            const uint3 c1 = *(const uint3*)(B.a[0][w][4 * hc + bp + 1] + 16 * l);
+            const v32h d =
+                __builtin_amdgcn_cvt_scalef32_pk32_f16_fp6((v6u){c0.x, c0.y, c0.z, c1.x, c1.y, c1.z}, 2.0f);
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const int jj = bp + kk;
+                const uint32_t scw = jj < 2 ? kh2.sc.x : kh2.sc.y;
+                const uint32_t sc = __builtin_amdgcn_perm(scw, scw, (jj & 1) ? 0x03020302u : 0x01000100u);  // (sc, sc)
+                A0[jj] = scaled8(d, 2 * kk, sc);
+                A1[jj] = scaled8(d, 2 * kk + 1, sc);
+            }
         }
-    }
-    // M's A: k = 4 kh .. 4 kh + 3 hold m of sub-blocks 2 kh, 2 kh, 2 kh + 1, 2 kh + 1 (each against a sum of 16)
-    const uint32_t mw = kh ? ks.m.y : ks.m.x;
-    const v4h Am = __builtin_bit_cast(v4h, make_uint2(__builtin_amdgcn_perm(mw, mw, 0x01000100u),
-                                                       __builtin_amdgcn_perm(mw, mw, 0x03020302u)));
+        // M's A: k = 4 kh .. 4 kh + 3 hold m of sub-blocks 2 kh, 2 kh, 2 kh + 1, 2 kh + 1 (each against a sum of 16)
+        const uint32_t mw = kh ? kh2.m.y : kh2.m.x;
+        const v4h Am = __builtin_bit_cast(v4h, make_uint2(__builtin_amdgcn_perm(mw, mw, 0x01000100u),
+                                                           __builtin_amdgcn_perm(mw, mw, 0x03020302u)));
 #pragma unroll
-    for (int t = 0; t < NTU; ++t) {
-        v16f P = z;
+        for (int t = 0; t < NTU; ++t) {
+            v16f P = z;
 #pragma unroll
-        for (int jj = 0; jj < KB; ++jj) {
-            const v8h B0 = *(const v8h*)(B.b[jj][t][0] + 16 * l);
-            const v8h B1 = *(const v8h*)(B.b[jj][t][1] + 16 * l);
-            P = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                A1[jj], B1, __builtin_amdgcn_mfma_f32_32x32x16_f16(A0[jj], B0, P, 0, 0, 0), 0, 0, 0);
-        }
-        const v4h Bm = *(const v4h*)&B.bs[32 * t + lr][4 * kh];
-        const v16f M = __builtin_amdgcn_mfma_f32_32x32x8f16(Am, Bm, z, 0, 0, 0);
-        const float dxv = B.dx[32 * t + lr];
+            for (int jj = 0; jj < 4; ++jj) {
+                const v8h B0 = *(const v8h*)(B.b[4 * hc + jj][t][0] + 16 * l);
+                const v8h B1 = *(const v8h*)(B.b[4 * hc + jj][t][1] + 16 * l);
+                P = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                    A1[jj], B1, __builtin_amdgcn_mfma_f32_32x32x16_f16(A0[jj], B0, P, 0, 0, 0), 0, 0, 0);
+            }
+            const v4h Bm = *(const v4h*)&B.bs[32 * t + lr][8 * hc + 4 * kh];
+            const v16f M = __builtin_amdgcn_mfma_f32_32x32x8f16(Am, Bm, z, 0, 0, 0);
+            const float dxv = B.dx[32 * t + lr];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const float mm = Dm[j] * M[j];
-            acc[0][t][j] = fmaf(fmaf(D[j], P[j], -mm), dxv, acc[0][t][j]);
+            for (int j = 0; j < 16; ++j) {
+                const float mm = Dm[j] * M[j];
+                acc[0][t][j] = fmaf(fmaf(D[j], P[j], -mm), dxv, acc[0][t][j]);
+            }
         }
     }
 }
@@ -534,18 +551,18 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
         const int8_t* xu = a.xq + (long long)in_row(min(ue, cnt - 1)) * K + 16 * uh;
         // the entry whose sums of 16 (threads 0..127) or scale (threads 128..191) this thread stages
         const long long br = in_row(min(tid & 63, cnt - 1));
-        const int* bsr = a.xbs + br * (K / 16) + 4 * ((tid >> 6) & 1);
-        const float* kdr = a.xd + (long long)in_row(min((tid - 128) & 63, cnt - 1)) * (K / 256);
-        KSc ks;
-        uint4 xb[KB / 2];
+        const int* bsr = a.xbs + br * (K / 16) + 4 * ((tid >> 6) & (KQ / 2 - 1));
+        const float* kdr = a.xd + br * (K / 256);
+        KSc<KQ> ks;
+        uint4 xb[KQ / 2];
         int4 bsv = {};
         float dxv = 0.0f;
-        for (int s = 0; s < nst; ++s) {
-            k_issue<NM, KB>(buf, s * KB, ks, vt[0], sct[0], xu, 32, xb, bsv, dxv, bsr, kdr, w, tid);
+        for (int s = 0; s < nb / KQ; ++s) {
+            k_issue<NM, KQ>(buf, s * KQ, ks, vt[0], sct[0], xu, 32, xb, bsv, dxv, bsr, kdr, w, tid);
             wait_vm<0>();
-            k_stage<NM, KB>(buf, xb, bsv, dxv, tid);
+            k_stage<NM, KQ>(buf, xb, bsv, dxv, tid);
             __syncthreads();
-            k_compute<NM, KB, NTU>(buf, ks, acc, w, l, lr, kh);
+            k_compute<NM, KQ, NTU>(buf, ks, acc, w, l, lr, kh);
             __syncthreads();
         }
     } else if constexpr (!F16) {
