@@ -11,6 +11,10 @@ extern "C" int moe_lib_ready(void);
 // Compute units of the initialised device (persistent grids size themselves by it)
 int moe_device_cus(void);
 
+struct qmatvec_q8;
+// gpu_swiglu's SwiGLU and quantized bundle without its argument checks; out may be null (no fp32 values written)
+hipError_t moe_swiglu_q8(const float* g, const float* u, float* out, int n, const qmatvec_q8* q8, hipStream_t stream);
+
 template <typename T>
 struct same_type {
     typedef T type;

@@ -11,6 +11,7 @@
 #include "fused_common.h"
 #include "gpu_ops.h"
 #include "grouped.h"
+#include "host_common.h"
 #include "qmatvec.h"
 
 struct FArgs;
@@ -47,7 +48,7 @@ size_t row_size(int type, int k) {
 
 // Scratch carve-up; every piece 256-byte aligned
 struct Plan {
-    size_t fused, logits, ids, wts, sg, qx, g, u, act, qa, down, sg_, su, sact, qs, sout, tok, pair, ntile, te, ts, tn,
+    size_t fused, logits, ids, wts, sg, qx, g, u, qa, down, sg_, su, qs, sout, tok, pair, ntile, te, ts, tn,
         gws, ynorm, total;
     int NS, qx_k, qa_k, qs_k, max_tiles, tile;
 };
@@ -80,12 +81,10 @@ Plan plan(const moe_layer_desc* d, int T) {
     p.qx = take(qmatvec_q8_bytes(p.qx_k));
     p.g = take((size_t)T * p.NS * FE * 4);
     p.u = take((size_t)T * p.NS * FE * 4);
-    p.act = take((size_t)T * p.NS * FE * 4);
     p.qa = take(qmatvec_q8_bytes(p.qa_k));
     p.down = take((size_t)T * p.NS * E * 4);
     p.sg_ = take(sh ? (size_t)T * FE * 4 : 0);
     p.su = take(sh ? (size_t)T * FE * 4 : 0);
-    p.sact = take(sh ? (size_t)T * FE * 4 : 0);
     p.qs = take(sh ? qmatvec_q8_bytes(p.qs_k) : 0);
     p.sout = take(sh ? (size_t)T * E * 4 : 0);
     p.tok = take((size_t)T * NU * 4);
@@ -146,7 +145,6 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
     float* sg = (float*)(s + p.sg);
     float* g = (float*)(s + p.g);
     float* u = (float*)(s + p.u);
-    float* act = (float*)(s + p.act);
     float* down = (float*)(s + p.down);
     qmatvec_q8 qx, qa, qs;
     qmatvec_q8_bind(&qx, s + p.qx, p.qx_k);
@@ -175,7 +173,7 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
                                          FE, E, T, st));
         else
             CHECK(qmatvec_launch_q8_id_pair(type, d->w_gate, d->w_up, rb_in, ids, ns, 0, &qx, g, u, FE, E, T, st));
-        CHECK(gpu_swiglu(g, u, act, T * ns * FE, &qa, st));
+        CHECK(moe_swiglu_q8(g, u, nullptr, T * ns * FE, &qa, st));
         if (slot)
             CHECK(qmatvec_launch_q8_id_x(type, d->w_down, nullptr, d->s_down, nullptr, rb_out, ids, ns, 1, &qa, down,
                                          nullptr, E, FE, T, st));
@@ -239,7 +237,7 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
                                      st));
             CHECK(moe_launch_entries(type, d->w_up, rb_in, &qx, u, FE, E, p.max_tiles, ntile, te, ts, tn, tok, pair,
                                      st));
-            CHECK(gpu_swiglu(g, u, act, T * NU * FE, &qa, st));
+            CHECK(moe_swiglu_q8(g, u, nullptr, T * NU * FE, &qa, st));
             CHECK(moe_launch_entries(type, d->w_down, rb_out, &qa, down, E, FE, p.max_tiles, ntile, te, ts, tn, pair,
                                      pair, st));
         } else {
@@ -247,7 +245,7 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
                                              ts, tn, tok, pair, st));
             CHECK(qmatvec_launch_q8_id_batch(type, d->w_up, rb_in, &qx, u, FE, E, p.max_tiles, p.tile, ntile, te, ts,
                                              tn, tok, pair, st));
-            CHECK(gpu_swiglu(g, u, act, T * NU * FE, &qa, st));
+            CHECK(moe_swiglu_q8(g, u, nullptr, T * NU * FE, &qa, st));
             CHECK(qmatvec_launch_q8_id_batch(type, d->w_down, rb_out, &qa, down, E, FE, p.max_tiles, p.tile, ntile, te,
                                              ts, tn, pair, pair, st));
         }
@@ -256,12 +254,11 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
     if (sh && !slot && !shared_done) {  // the shared expert as a dense FFN on all T tokens, then the combine
         float* sgt = (float*)(s + p.sg_);
         float* sut = (float*)(s + p.su);
-        float* sact = (float*)(s + p.sact);
         float* sout = (float*)(s + p.sout);
         qmatvec_q8_bind(&qs, s + p.qs, p.qs_k);
         CHECK(qmatvec_launch_q8_batch(type, d->s_gate, rb_in, &qx, sgt, FE, FE, E, T, st));
         CHECK(qmatvec_launch_q8_batch(type, d->s_up, rb_in, &qx, sut, FE, FE, E, T, st));
-        CHECK(gpu_swiglu(sgt, sut, sact, T * FE, &qs, st));
+        CHECK(moe_swiglu_q8(sgt, sut, nullptr, T * FE, &qs, st));
         CHECK(qmatvec_launch_q8_batch(type, d->s_down, rb_out, &qs, sout, E, E, FE, T, st));
         CHECK(gpu_moe_combine(down, wts, sout, d->w_shexp ? sg : nullptr, out, NU, E, T, st));
     }

@@ -95,4 +95,60 @@ __device__ __forceinline__ void q8_quantize_256(float v, bool active, long long 
     }
 }
 
+// The same outputs from one wave per 256-value block, the whole block valid: lane l holds values 4 l .. 4 l + 3, so
+// a Q8_0 block is eight lanes and the Q8_K block the wave, with no LDS and no barrier. The expressions are
+// q8_quantize_256's, and every reduction gives the same result in any pairing (maxima, the arg-max's total order,
+// integer sums), so the outputs are the same bits; the stores are four bytes a lane.
+__device__ __forceinline__ void q8_quantize_256_wave(const float (&v)[4], long long blk, int lane, const Q8Out& o) {
+    const long long i0 = blk * 256 + 4 * lane;
+    float a = fabsf(v[0]);
+#pragma unroll
+    for (int j = 1; j < 4; ++j) a = fmaxf(a, fabsf(v[j]));
+    const float am = group_max<8>(a);
+    const float id = am != 0.0f ? 127.0f / am : 0.0f;
+    int q0[4], s = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        q0[j] = (int)rintf(v[j] * id);
+        s += q0[j];
+    }
+    s = group_sum_i<8>(s);
+    *(uint32_t*)(o.q0 + i0) =
+        (q0[0] & 0xff) | ((q0[1] & 0xff) << 8) | ((q0[2] & 0xff) << 16) | ((uint32_t)q0[3] << 24);
+    if ((lane & 7) == 0) {
+        const float d = am / 127.0f;
+        o.d0[blk * 8 + (lane >> 3)] = fp16_round(d);
+        o.s0[blk * 8 + (lane >> 3)] = __float_as_int(fp16_round(d * (float)s));
+    }
+
+    float ba = fabsf(v[0]), bv = v[0];
+    int bi = 4 * lane;
+#pragma unroll
+    for (int j = 1; j < 4; ++j)  // (strictly larger: the lower index stays on ties)
+        if (fabsf(v[j]) > ba) {
+            ba = fabsf(v[j]);
+            bv = v[j];
+            bi = 4 * lane + j;
+        }
+    argmax_step<1>(ba, bv, bi);
+    argmax_step<2>(ba, bv, bi);
+    argmax_step<4>(ba, bv, bi);
+    argmax_step<8>(ba, bv, bi);
+    argmax_step<16>(ba, bv, bi);
+    argmax_step<32>(ba, bv, bi);
+    int q[4] = {0, 0, 0, 0}, s16 = 0;
+    float iscale = 0.0f;
+    if (ba != 0.0f) {
+        iscale = -127.0f / bv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[j] = min(127, (int)rintf(iscale * v[j]));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s16 += q[j];
+    s16 = group_sum_i<4>(s16);
+    *(uint32_t*)(o.qK + i0) = (q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) | ((uint32_t)q[3] << 24);
+    if (lane == 0) o.dK[blk] = ba != 0.0f ? 1.0f / iscale : 0.0f;
+    if ((lane & 3) == 0) o.bsK[blk * 16 + (lane >> 2)] = s16;
+}
+
 #endif  // Q8_QUANT_H

@@ -50,6 +50,20 @@ __global__ void __launch_bounds__(256) k_quantize_q8(const float* x, int n, Q8Ou
     q8_quantize_256(v, act, blockIdx.x, t, sh, o);
 }
 
+// The same bundle for n % 256 == 0 and 16-byte aligned x: one wave per 256-value block (q8_quantize_256_wave),
+// four blocks a workgroup, 16-byte loads
+__global__ void __launch_bounds__(256) k_quantize_q8_w(const float* x, long long nblk, Q8Out o) {
+    const long long blk = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= nblk) return;  // (whole waves)
+    const int lane = threadIdx.x & 63;
+    const float4 p = *(const float4*)(x + blk * 256 + 4 * lane);
+    const float v[4] = {p.x, p.y, p.z, p.w};
+    if (o.xh)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) half_copy(o, blk * 256 + 4 * lane + j, v[j]);
+    q8_quantize_256_wave(v, blk, lane, o);
+}
+
 // Q8_0 values and scales only (the Q8_0-activation types need no Q8_1 sums or Q8_K): 2,048 values per
 // workgroup, the quantizer's expressions (the same bits as k_quantize_q8's Q8_0 part)
 __global__ void __launch_bounds__(256) k_quantize_q8_0(const float* x, int n, int8_t* q0, float* d0) {
@@ -67,10 +81,29 @@ __global__ void __launch_bounds__(256) k_swiglu(const float* g, const float* u, 
     if (i < n) {
         const float a = g[i];
         v = a / (1.0f + __expf(-a)) * u[i];
-        out[i] = v;
+        if (out) out[i] = v;
         half_copy(o, i, v);
     }
     q8_quantize_256(v, i < n, blockIdx.x, t, sh, o);
+}
+
+// The same for n % 256 == 0 and 16-byte aligned rows: a wave per 256-value block (q8_quantize_256_wave); out may be
+// null (the layer's own SwiGLU, whose fp32 values nothing reads)
+__global__ void __launch_bounds__(256) k_swiglu_w(const float* g, const float* u, float* out, long long nblk, Q8Out o) {
+    const long long blk = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= nblk) return;  // (whole waves)
+    const int lane = threadIdx.x & 63;
+    const long long i0 = blk * 256 + 4 * lane;
+    const float4 g4 = *(const float4*)(g + i0), u4 = *(const float4*)(u + i0);
+    const float gg[4] = {g4.x, g4.y, g4.z, g4.w}, uu[4] = {u4.x, u4.y, u4.z, u4.w};
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = gg[j] / (1.0f + __expf(-gg[j])) * uu[j];
+    if (out) *(float4*)(out + i0) = make_float4(v[0], v[1], v[2], v[3]);
+    if (o.xh)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) half_copy(o, i0 + j, v[j]);
+    if (o.qK) q8_quantize_256_wave(v, blk, lane, o);
 }
 
 // ------------------------------------------------------------------ combine (src/gpu_ops.hip:245-264)
@@ -377,6 +410,9 @@ extern "C" void qmatvec_q8_bind(qmatvec_q8* q, void* mem, int max_k) {
 extern "C" hipError_t qmatvec_quantize(const float* x, int K, const qmatvec_q8* q, hipStream_t stream) {
     if (!moe_lib_ready()) return hipErrorNotInitialized;
     if (!q || K <= 0 || K % 32 != 0 || K > q->max_k) return hipErrorInvalidValue;
+    if (K % 256 == 0 && ((uintptr_t)x & 15) == 0)
+        return launch_kernel(k_quantize_q8_w, dim3((K / 256 + 3) / 4), dim3(256), 0, stream, x, (long long)K / 256,
+                             q8_out(q));
     return launch_kernel(k_quantize_q8, dim3((K + 255) / 256), dim3(256), 0, stream, x, K, q8_out(q));
 }
 
@@ -416,6 +452,13 @@ extern "C" hipError_t gpu_swiglu(const float* g, const float* u, float* out, int
                                  hipStream_t stream) {
     if (!moe_lib_ready()) return hipErrorNotInitialized;
     if (n <= 0 || (q8 && (n % 32 != 0 || n > q8->max_k))) return hipErrorInvalidValue;
+    return moe_swiglu_q8(g, u, out, n, q8, stream);
+}
+
+hipError_t moe_swiglu_q8(const float* g, const float* u, float* out, int n, const qmatvec_q8* q8, hipStream_t stream) {
+    if (n % 256 == 0 && (((uintptr_t)g | (uintptr_t)u | (uintptr_t)out) & 15) == 0)
+        return launch_kernel(k_swiglu_w, dim3((n / 256 + 3) / 4), dim3(256), 0, stream, g, u, out, (long long)n / 256,
+                             q8_out(q8));
     return launch_kernel(k_swiglu, dim3((n + 255) / 256), dim3(256), 0, stream, g, u, out, n, q8_out(q8));
 }
 
