@@ -98,6 +98,7 @@ struct GArgs {
 #define GG_KB2 4  // the same for the gate / up / SwiGLU kernel (two matrices per stage)
 #endif
 #define GG_NT (GG_TILE / 32)
+#define GG_TRS 36  // floats per entry of the output transpose (32 rows + 4: 16-byte aligned, banks spread)
 #ifndef GG_XCD_RANGES
 #define GG_XCD_RANGES 1  // each XCD takes a contiguous range of work items (0: round-robin, the dispatch order)
 #endif
@@ -609,13 +610,36 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
     }
     // acc[m][t][j] is C[row 8 (j / 4) + 4 kh + j % 4][entry 32 t + lr] of the wave's 32 x GG_TILE block
     if constexpr (NM == 1) {
+        if (((uintptr_t)a.y | (uintptr_t)(a.ldy * 4)) & 15) {  // (uniform) rows not 16-byte aligned: 4-byte stores
 #pragma unroll
-        for (int t = 0; t < NTU; ++t)
-            if (32 * t + lr < cnt) {
-                float* y = a.y + (long long)out_row(32 * t + lr) * a.ldy + r0;
+            for (int t = 0; t < NTU; ++t)
+                if (32 * t + lr < cnt) {
+                    float* y = a.y + (long long)out_row(32 * t + lr) * a.ldy + r0;
 #pragma unroll
-                for (int j = 0; j < 16; ++j) y[8 * (j >> 2) + 4 * kh + (j & 3)] = acc[0][t][j];
+                    for (int j = 0; j < 16; ++j) y[8 * (j >> 2) + 4 * kh + (j & 3)] = acc[0][t][j];
+                }
+        } else {
+            // each 32 x 32 block turned through this wave's part of the (now idle) stage buffer, so that a store
+            // writes 16 bytes a lane and whole 128-byte rows of 32 outputs (8 per store), not 8 bytes of 32 rows
+            float* tr = (float*)&buf + w * 32 * GG_TRS;
+#pragma unroll
+            for (int t = 0; t < NTU; ++t) {
+                const int orow = 32 * t + lr < cnt ? out_row(32 * t + lr) : 0;  // lane lr: entry 32 t + lr's row
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *(float4*)&tr[lr * GG_TRS + 8 * q + 4 * kh] =
+                        make_float4(acc[0][t][4 * q], acc[0][t][4 * q + 1], acc[0][t][4 * q + 2], acc[0][t][4 * q + 3]);
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);  // (a wave's LDS operations complete in order)
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const int e = (l >> 3) + 8 * p;  // entry of the tile; this lane's rows 4 (l % 8) .. + 3
+                    const float4 v = *(const float4*)&tr[e * GG_TRS + 4 * (l & 7)];
+                    const int oe = __shfl(orow, e, 64);
+                    if (32 * t + e < cnt) *(float4*)(a.y + (long long)oe * a.ldy + r0 + 4 * (l & 7)) = v;
+                }
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);
             }
+        }
     } else {
 #pragma unroll
         for (int t = 0; t < NTU; ++t) {
