@@ -410,7 +410,7 @@ extern "C" void qmatvec_q8_bind(qmatvec_q8* q, void* mem, int max_k) {
 extern "C" hipError_t qmatvec_quantize(const float* x, int K, const qmatvec_q8* q, hipStream_t stream) {
     if (!moe_lib_ready()) return hipErrorNotInitialized;
     if (!q || K <= 0 || K % 32 != 0 || K > q->max_k) return hipErrorInvalidValue;
-    if (K % 256 == 0 && ((uintptr_t)x & 15) == 0)
+    if (K % 256 == 0 && aligned(x, 16) && aligned(q->q0, 4) && aligned(q->qK, 4))
         return launch_kernel(k_quantize_q8_w, dim3((K / 256 + 3) / 4), dim3(256), 0, stream, x, (long long)K / 256,
                              q8_out(q));
     return launch_kernel(k_quantize_q8, dim3((K + 255) / 256), dim3(256), 0, stream, x, K, q8_out(q));
@@ -456,7 +456,8 @@ extern "C" hipError_t gpu_swiglu(const float* g, const float* u, float* out, int
 }
 
 hipError_t moe_swiglu_q8(const float* g, const float* u, float* out, int n, const qmatvec_q8* q8, hipStream_t stream) {
-    if (n % 256 == 0 && (((uintptr_t)g | (uintptr_t)u | (uintptr_t)out) & 15) == 0)
+    if (n % 256 == 0 && (((uintptr_t)g | (uintptr_t)u | (uintptr_t)out) & 15) == 0 &&
+        (!q8 || (aligned(q8->q0, 4) && aligned(q8->qK, 4))))
         return launch_kernel(k_swiglu_w, dim3((n / 256 + 3) / 4), dim3(256), 0, stream, g, u, out, (long long)n / 256,
                              q8_out(q8));
     return launch_kernel(k_swiglu, dim3((n + 255) / 256), dim3(256), 0, stream, g, u, out, n, q8_out(q8));
