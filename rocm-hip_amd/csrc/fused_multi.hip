@@ -440,7 +440,7 @@ hipError_t launch_multi(const FArgs& a, const qmatvec_q8* qa, int kernels, hipSt
             e = launch_kernel(k_fm_gate_up<TYPE, LI, NI>, dim3(pairs < cus ? pairs : cus), dim3(1024), 0, st, a);
     }
     if (Fmt<TYPE>::Q8K && e == hipSuccess && (kernels & 2))
-        e = moe_swiglu_q8(a.g, a.u, nullptr, a.T * a.NS * a.FE, qa, st);
+        e = moe_swiglu_q8(a.g, a.u, nullptr, a.T * a.NS * a.FE, qa, st, 2);  // (Q4_K: Q8_K only)
     // down + combine: per token (the T = 1 kernel over T rows of workgroups, one wave per slot) for Q8_0 and up to
     // T = 3; the item-list kernel for the 4-bit types from T = 4 (its 8-row workgroups share an expert's rows among
     // the tokens that chose it: config 1 T = 4 43.6 against 44.4 µs, T = 7 65.5 against 67.7). Q8_0's units

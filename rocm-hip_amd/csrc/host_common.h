@@ -12,8 +12,10 @@ extern "C" int moe_lib_ready(void);
 int moe_device_cus(void);
 
 struct qmatvec_q8;
-// gpu_swiglu's SwiGLU and quantized bundle without its argument checks; out may be null (no fp32 values written)
-hipError_t moe_swiglu_q8(const float* g, const float* u, float* out, int n, const qmatvec_q8* q8, hipStream_t stream);
+// gpu_swiglu's SwiGLU and quantized bundle without its argument checks; out may be null (no fp32 values written);
+// parts: the bundle's formats wanted (1: Q8_0 + Q8_1 sums, 2: Q8_K, 3: both; lengths not a multiple of 256 get both)
+hipError_t moe_swiglu_q8(const float* g, const float* u, float* out, int n, const qmatvec_q8* q8, hipStream_t stream,
+                         int parts);
 
 template <typename T>
 struct same_type {

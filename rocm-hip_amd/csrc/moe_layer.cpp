@@ -25,6 +25,7 @@ bool moe_fused_multi_try(const moe_layer_desc* d, const float* x, const float* l
 
 
 hipError_t moe_quantize_q8_0(const float* x, int n, const qmatvec_q8* q, hipStream_t stream);
+hipError_t moe_quantize_q8k(const float* x, int n, const qmatvec_q8* q, hipStream_t stream);
 
 static std::atomic<int> g_fused{1};
 
@@ -158,7 +159,7 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
         CHECK(qmatvec_launch_batch(0, d->w_router, (size_t)E * 4, x, lg, NE, E, T, st));
     if (!front) {
     } else if (type == 12) {  // Q4_K reads Q8_K activations; the others read Q8_0 values and scales only
-        CHECK(qmatvec_quantize(x, T * E, &qx, st));
+        CHECK(moe_quantize_q8k(x, T * E, &qx, st));
     } else {
         CHECK(moe_quantize_q8_0(x, T * E, &qx, st));
     }
@@ -173,7 +174,7 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
                                          FE, E, T, st));
         else
             CHECK(qmatvec_launch_q8_id_pair(type, d->w_gate, d->w_up, rb_in, ids, ns, 0, &qx, g, u, FE, E, T, st));
-        CHECK(moe_swiglu_q8(g, u, nullptr, T * ns * FE, &qa, st));
+        CHECK(moe_swiglu_q8(g, u, nullptr, T * ns * FE, &qa, st, type == 12 ? 2 : 1));
         if (slot)
             CHECK(qmatvec_launch_q8_id_x(type, d->w_down, nullptr, d->s_down, nullptr, rb_out, ids, ns, 1, &qa, down,
                                          nullptr, E, FE, T, st));
@@ -237,7 +238,7 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
                                      st));
             CHECK(moe_launch_entries(type, d->w_up, rb_in, &qx, u, FE, E, p.max_tiles, ntile, te, ts, tn, tok, pair,
                                      st));
-            CHECK(moe_swiglu_q8(g, u, nullptr, T * NU * FE, &qa, st));
+            CHECK(moe_swiglu_q8(g, u, nullptr, T * NU * FE, &qa, st, type == 12 ? 2 : 1));
             CHECK(moe_launch_entries(type, d->w_down, rb_out, &qa, down, E, FE, p.max_tiles, ntile, te, ts, tn, pair,
                                      pair, st));
         } else {
@@ -245,7 +246,7 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
                                              ts, tn, tok, pair, st));
             CHECK(qmatvec_launch_q8_id_batch(type, d->w_up, rb_in, &qx, u, FE, E, p.max_tiles, p.tile, ntile, te, ts,
                                              tn, tok, pair, st));
-            CHECK(moe_swiglu_q8(g, u, nullptr, T * NU * FE, &qa, st));
+            CHECK(moe_swiglu_q8(g, u, nullptr, T * NU * FE, &qa, st, type == 12 ? 2 : 1));
             CHECK(qmatvec_launch_q8_id_batch(type, d->w_down, rb_out, &qa, down, E, FE, p.max_tiles, p.tile, ntile, te,
                                              ts, tn, pair, pair, st));
         }
@@ -258,7 +259,7 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
         qmatvec_q8_bind(&qs, s + p.qs, p.qs_k);
         CHECK(qmatvec_launch_q8_batch(type, d->s_gate, rb_in, &qx, sgt, FE, FE, E, T, st));
         CHECK(qmatvec_launch_q8_batch(type, d->s_up, rb_in, &qx, sut, FE, FE, E, T, st));
-        CHECK(moe_swiglu_q8(sgt, sut, nullptr, T * FE, &qs, st));
+        CHECK(moe_swiglu_q8(sgt, sut, nullptr, T * FE, &qs, st, type == 12 ? 2 : 1));
         CHECK(qmatvec_launch_q8_batch(type, d->s_down, rb_out, &qs, sout, E, E, FE, T, st));
         CHECK(gpu_moe_combine(down, wts, sout, d->w_shexp ? sg : nullptr, out, NU, E, T, st));
     }

@@ -95,12 +95,8 @@ __device__ __forceinline__ void q8_quantize_256(float v, bool active, long long 
     }
 }
 
-// The same outputs from one wave per 256-value block, the whole block valid: lane l holds values 4 l .. 4 l + 3, so
-// a Q8_0 block is eight lanes and the Q8_K block the wave, with no LDS and no barrier. The expressions are
-// q8_quantize_256's, and every reduction gives the same result in any pairing (maxima, the arg-max's total order,
-// integer sums), so the outputs are the same bits; the stores are four bytes a lane.
-__device__ __forceinline__ void q8_quantize_256_wave(const float (&v)[4], long long blk, int lane, const Q8Out& o) {
-    const long long i0 = blk * 256 + 4 * lane;
+// The Q8_0 part of q8_quantize_256_wave (values, scales, Q8_1 sums)
+__device__ __forceinline__ void q8_0_256_wave(const float (&v)[4], long long blk, int lane, long long i0, const Q8Out& o) {
     float a = fabsf(v[0]);
 #pragma unroll
     for (int j = 1; j < 4; ++j) a = fmaxf(a, fabsf(v[j]));
@@ -120,7 +116,10 @@ __device__ __forceinline__ void q8_quantize_256_wave(const float (&v)[4], long l
         o.d0[blk * 8 + (lane >> 3)] = fp16_round(d);
         o.s0[blk * 8 + (lane >> 3)] = __float_as_int(fp16_round(d * (float)s));
     }
+}
 
+// The Q8_K part of q8_quantize_256_wave (values, scale, sums of 16)
+__device__ __forceinline__ void q8_k_256_wave(const float (&v)[4], long long blk, int lane, long long i0, const Q8Out& o) {
     float ba = fabsf(v[0]), bv = v[0];
     int bi = 4 * lane;
 #pragma unroll
@@ -149,6 +148,17 @@ __device__ __forceinline__ void q8_quantize_256_wave(const float (&v)[4], long l
     *(uint32_t*)(o.qK + i0) = (q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) | ((uint32_t)q[3] << 24);
     if (lane == 0) o.dK[blk] = ba != 0.0f ? 1.0f / iscale : 0.0f;
     if ((lane & 3) == 0) o.bsK[blk * 16 + (lane >> 2)] = s16;
+}
+
+// The same outputs from one wave per 256-value block, the whole block valid: lane l holds values 4 l .. 4 l + 3, so
+// a Q8_0 block is eight lanes and the Q8_K block the wave, with no LDS and no barrier. The expressions are
+// q8_quantize_256's, and every reduction gives the same result in any pairing (maxima, the arg-max's total order,
+// integer sums), so the outputs are the same bits; the stores are four bytes a lane. A null o.q0 / o.qK skips that
+// format (uniform).
+__device__ __forceinline__ void q8_quantize_256_wave(const float (&v)[4], long long blk, int lane, const Q8Out& o) {
+    const long long i0 = blk * 256 + 4 * lane;
+    if (o.q0) q8_0_256_wave(v, blk, lane, i0, o);
+    if (o.qK) q8_k_256_wave(v, blk, lane, i0, o);
 }
 
 #endif  // Q8_QUANT_H

@@ -103,7 +103,7 @@ __global__ void __launch_bounds__(256) k_swiglu_w(const float* g, const float* u
     if (o.xh)
 #pragma unroll
         for (int j = 0; j < 4; ++j) half_copy(o, i0 + j, v[j]);
-    if (o.qK) q8_quantize_256_wave(v, blk, lane, o);
+    q8_quantize_256_wave(v, blk, lane, o);
 }
 
 // ------------------------------------------------------------------ combine (src/gpu_ops.hip:245-264)
@@ -452,14 +452,23 @@ extern "C" hipError_t gpu_swiglu(const float* g, const float* u, float* out, int
                                  hipStream_t stream) {
     if (!moe_lib_ready()) return hipErrorNotInitialized;
     if (n <= 0 || (q8 && (n % 32 != 0 || n > q8->max_k))) return hipErrorInvalidValue;
-    return moe_swiglu_q8(g, u, out, n, q8, stream);
+    return moe_swiglu_q8(g, u, out, n, q8, stream, 3);
 }
 
-hipError_t moe_swiglu_q8(const float* g, const float* u, float* out, int n, const qmatvec_q8* q8, hipStream_t stream) {
+// The bundle with only the formats in parts (1: Q8_0 + Q8_1 sums, 2: Q8_K) on the wave-per-block path
+static Q8Out q8_out_parts(const qmatvec_q8* q, int parts) {
+    Q8Out o = q8_out(q);
+    if (!(parts & 1)) o.q0 = nullptr;
+    if (!(parts & 2)) o.qK = nullptr;
+    return o;
+}
+
+hipError_t moe_swiglu_q8(const float* g, const float* u, float* out, int n, const qmatvec_q8* q8, hipStream_t stream,
+                         int parts) {
     if (n % 256 == 0 && (((uintptr_t)g | (uintptr_t)u | (uintptr_t)out) & 15) == 0 &&
         (!q8 || (aligned(q8->q0, 4) && aligned(q8->qK, 4))))
         return launch_kernel(k_swiglu_w, dim3((n / 256 + 3) / 4), dim3(256), 0, stream, g, u, out, (long long)n / 256,
-                             q8_out(q8));
+                             q8_out_parts(q8, parts));
     return launch_kernel(k_swiglu, dim3((n + 255) / 256), dim3(256), 0, stream, g, u, out, n, q8_out(q8));
 }
 
@@ -490,6 +499,17 @@ extern "C" hipError_t gpu_moe_combine_scaled(const float* down, const float* wts
 extern "C" hipError_t gpu_moe_combine(const float* down, const float* wts, const float* shared, const float* sg,
                                       float* out, int n_used, int n, int T, hipStream_t stream) {
     return gpu_moe_combine_scaled(down, wts, shared, sg, nullptr, nullptr, out, n_used, n, T, stream);
+}
+
+// Internal (moe_layer_forward, Q4_K): x's Q8_K part only (n % 256 == 0, n <= q->max_k); qmatvec_quantize's
+// kernels and bits
+hipError_t moe_quantize_q8k(const float* x, int n, const qmatvec_q8* q, hipStream_t stream) {
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (n <= 0 || n % 256 || !q || n > q->max_k) return hipErrorInvalidValue;
+    if (aligned(x, 16) && aligned(q->qK, 4))
+        return launch_kernel(k_quantize_q8_w, dim3((n / 256 + 3) / 4), dim3(256), 0, stream, x, (long long)n / 256,
+                             q8_out_parts(q, 2));
+    return launch_kernel(k_quantize_q8, dim3((n + 255) / 256), dim3(256), 0, stream, x, n, q8_out(q));
 }
 
 // Internal (moe_layer_forward): Q8_0 values and scales of x [n] into q (n % 32 == 0, n <= q->max_k)
