@@ -466,9 +466,12 @@ template <int TYPE, int NM, int KB>
 #ifndef GG_WPE
 #define GG_WPE 3  // waves per SIMD asked of the compiler (0: its choice; 3 measured 3-8% faster than its 2)
 #endif
+#ifndef GG_WPE_D8
+#define GG_WPE_D8 5  // the same for the one-matrix Q8_0 kernel (96 VGPRs: five workgroups per CU)
+#endif
 __global__ void __launch_bounds__(256)
 #if GG_WPE
-__attribute__((amdgpu_waves_per_eu(GG_WPE)))
+__attribute__((amdgpu_waves_per_eu(TYPE == QT_Q8_0 && NM == 1 ? GG_WPE_D8 : GG_WPE)))
 #endif
 k_grouped(GArgs a) {
     __shared__ __attribute__((aligned(1024))) typename BufOf<TYPE, NM, KB>::type buf;
