@@ -624,6 +624,7 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
         } else {
             // each 32 x 32 block turned through this wave's part of the (now idle) stage buffer, so that a store
             // writes 16 bytes a lane and whole 128-byte rows of 32 outputs (8 per store), not 8 bytes of 32 rows
+            static_assert(sizeof(buf) >= 4 * 32 * GG_TRS * sizeof(float), "four waves' 32 x 32 blocks fit the buffer");
             float* tr = (float*)&buf + w * 32 * GG_TRS;
 #pragma unroll
             for (int t = 0; t < NTU; ++t) {
