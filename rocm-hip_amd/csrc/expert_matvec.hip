@@ -323,9 +323,10 @@ bool find_packed(const void* W, int type, int K, size_t row_bytes, const uint8_t
 }
 
 // The MFMA operand tiles of the registered matrix whose native rows start at W (at a 32-row group boundary): the
-// value tiles and scale tiles of W's first row group and their bytes per 32-row group, or false
+// value tiles and scale tiles of W's first row group and their bytes per 32-row group (and, when rows_from_w is
+// given, the registered rows from W on), or false
 bool find_tiles(const void* W, int type, int K, size_t row_bytes, const uint8_t** vt, const uint8_t** st,
-                long long* vgs, long long* sgs) {
+                long long* vgs, long long* sgs, long long* rows_from_w = nullptr) {
     if (!W) return false;
     std::lock_guard<std::mutex> lk(g_pack_mu);
     auto it = g_packed.upper_bound((uintptr_t)W);
@@ -341,6 +342,7 @@ bool find_tiles(const void* W, int type, int K, size_t row_bytes, const uint8_t*
     *st = p.tiles + (size_t)p.rows * tile_value_row(type, K) + g * 32 * tile_scale_row(type, K);
     *vgs = 32ll * tile_value_row(type, K);
     *sgs = 32ll * tile_scale_row(type, K);
+    if (rows_from_w) *rows_from_w = p.rows - 32 * g;
     return true;
 }
 
@@ -764,10 +766,10 @@ extern "C" hipError_t qmatvec_launch_q8_batch(int type, const void* W, size_t ro
 // Entry tiles of the grouped kernels (the MFMA kernel's 64; the per-entry fallback takes any)
 #define ENTRY_TILE 64
 
-hipError_t moe_launch_entries(int type, const void* W, size_t row_bytes, const qmatvec_q8* q, float* y, int N, int K,
-                              int max_tiles, const int32_t* n_tiles, const int32_t* tile_e, const int32_t* tile_start,
-                              const int32_t* tile_n, const int32_t* in_rows, const int32_t* out_rows,
-                              hipStream_t stream) {
+static hipError_t moe_launch_entries(int type, const void* W, size_t row_bytes, const qmatvec_q8* q, float* y, int N,
+                                     int K, int max_tiles, const int32_t* n_tiles, const int32_t* tile_e,
+                                     const int32_t* tile_start, const int32_t* tile_n, const int32_t* in_rows,
+                                     const int32_t* out_rows, hipStream_t stream) {
     MvArgs a = {};
     const void* Ws[4] = {W, nullptr, nullptr, nullptr};
     const int bw = bind_weights(a, type, K, row_bytes, Ws);
@@ -817,8 +819,13 @@ extern "C" hipError_t qmatvec_launch_q8_id_batch(int type, const void* W, size_t
         return hipErrorInvalidValue;
     if (!W || !q || row_bytes != native_row(type, K) || !aligned(W, 4)) return hipErrorInvalidValue;
     const uint8_t *v = nullptr, *s = nullptr;
-    long long vgs = 0, sgs = 0;
-    if (moe_grouped_mfma_ok(type, N, K) && find_tiles(W, type, K, row_bytes, &v, &s, &vgs, &sgs))
+    long long vgs = 0, sgs = 0, rows = 0;
+    // Q4_K with fewer entries than 3/4 of the experts (max_tiles = gpu_moe_max_tiles(T, n_used, n_expert, tile) is
+    // then T n_used, and the registration holds n_expert N rows from W): the per-entry kernel, whose rows go through
+    // the sub-block decode once per entry, beats 64-entry MFMA tiles left mostly empty (config 3's layer shape,
+    // gate + up + SwiGLU + down + routing: T 8 103 against 160 us, T 16 165 against 187, even at T 24 = 0.75 x 256 / 8)
+    if (moe_grouped_mfma_ok(type, N, K) && find_tiles(W, type, K, row_bytes, &v, &s, &vgs, &sgs, &rows) &&
+        (type != QT_Q4_K || 4ll * max_tiles >= 3 * (rows / N)))
         return moe_launch_grouped_mfma(type, v, s, vgs, sgs, q, y, N, K,
                                        max_tiles, n_tiles, tile_e, tile_start, tile_n, in_rows, out_rows, 0, nullptr,
                                        stream);

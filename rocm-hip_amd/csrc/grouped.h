@@ -35,13 +35,6 @@ hipError_t moe_launch_grouped_swiglu(int type, const uint8_t* vg, const uint8_t*
 hipError_t moe_launch_dense_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
                                  const qmatvec_q8* q, float* y, long long ldy, int N, int K, int T,
                                  hipStream_t stream);
-// The per-entry kernel for a grouped launch whatever the matrix's tiles (the caller picks it where it is faster)
-hipError_t moe_launch_entries(int type, const void* W, size_t row_bytes, const qmatvec_q8* q, float* y, int N, int K,
-                              int max_tiles, const int32_t* n_tiles, const int32_t* tile_e, const int32_t* tile_start,
-                              const int32_t* tile_n, const int32_t* in_rows, const int32_t* out_rows,
-                              hipStream_t stream);
-// Fewest tokens of a batch for which a Q4_K layer's grouped launches run on the MFMA kernel
-#define Q4K_MFMA_MIN_T 24
 bool moe_packed_tiles(const void* W, int type, int K, size_t row_bytes, const uint8_t** vt, const uint8_t** st,
                       long long* vgs, long long* sgs);
 

@@ -230,17 +230,6 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
                                       st));
                 shared_done = true;
             }
-        } else if (type == 12 && T < Q4K_MFMA_MIN_T) {
-            // Q4_K below Q4K_MFMA_MIN_T tokens (under 0.75 entries per expert at 256 experts top-8): the per-entry
-            // kernel, whose weights go through the sub-block decode once per entry, beats the MFMA kernel's 64-row
-            // tiles that stay mostly empty (measured at config 3: T 8 103 vs 160 us, T 16 165 vs 187, T 24 even)
-            CHECK(moe_launch_entries(type, d->w_gate, rb_in, &qx, g, FE, E, p.max_tiles, ntile, te, ts, tn, tok, pair,
-                                     st));
-            CHECK(moe_launch_entries(type, d->w_up, rb_in, &qx, u, FE, E, p.max_tiles, ntile, te, ts, tn, tok, pair,
-                                     st));
-            CHECK(moe_swiglu_q8(g, u, nullptr, T * NU * FE, &qa, st, type == 12 ? 2 : 1));
-            CHECK(moe_launch_entries(type, d->w_down, rb_out, &qa, down, E, FE, p.max_tiles, ntile, te, ts, tn, pair,
-                                     pair, st));
         } else {
             CHECK(qmatvec_launch_q8_id_batch(type, d->w_gate, rb_in, &qx, g, FE, E, p.max_tiles, p.tile, ntile, te,
                                              ts, tn, tok, pair, st));
