@@ -108,6 +108,12 @@ hipError_t qmatvec_launch_q8_pair(int type, const void *W, int N, float *y, cons
 hipError_t qmatvec_launch_q8_batch(int type, const void *W, size_t row_bytes, const qmatvec_q8 *q, float *y,
                                    long long ldy, int N, int K, int T, hipStream_t stream);
 
+// No counterpart in the reference (a test hook). Which kernel qmatvec_launch_q8_batch gives a registered matrix
+// from T = 8 tokens: 0 (the default) the one estimated faster, the MFMA kernel (a chain of K / 128 stages, its
+// weights read once per 64 tokens) or the matvec kernel (the weights once per token); 1 always the MFMA kernel;
+// 2 always the matvec kernel. Process-wide; the outputs agree within fp32 reordering either way.
+void qmatvec_dense_mfma_mode(int mode);
+
 // Replaces src/qmatvec.h:156-157. Mixture-of-experts matvecs with the expert choice read from device memory:
 // W stacks every expert's N rows; for token t and slot j < n_used, expert e = ids[t * n_used + j] multiplies
 // input row t (x_per_slot = 0) or t * n_used + j (x_per_slot = 1) of q into row t * n_used + j of y.

@@ -10,6 +10,7 @@
 // e * N .. of W), input row t (x_per_slot 0) or t * n_used + j (1), output row t * n_used + j; grid.y >=
 // n_used selects the second matrix (W2 -> y2); e = -1 selects the extra matrix Wx / W2x.
 
+#include <atomic>
 #include <map>
 #include <mutex>
 
@@ -749,16 +750,31 @@ extern "C" hipError_t qmatvec_launch_q8(int type, const void* W, size_t row_byte
     return dense(type, W, N, y, nullptr, 0, nullptr, row_bytes, q, K, 1, N, stream);
 }
 
-// From T = 8 tokens a registered matrix runs on the MFMA kernel (its weights read once for 64 tokens), below it
-// on the matvec kernel (weights once per token, from L2 after the first)
-#define DENSE_MFMA_MIN_T 8
+// A registered matrix runs T tokens on the MFMA kernel when that is estimated faster than the matvec kernel. The
+// MFMA launch is a chain of K / 128 stages of ~1.8 us each whatever T, over (N / 128) ceil(T / 64) workgroups
+// (about 768 resident at once); the matvec kernel reads the matrix once per token from L2, at ~18 TB/s for Q8_0 rows,
+// ~9.5 for Q4_K and ~6 for the FP4 types (their decode). Measured (N 768, K 2048; Q4_K N 1024, K 3072), us per
+// launch, matvec / MFMA: Q8_0 T 64 8.2 / 28.8, T 256 22.8 / 28.9, T 512 43.2 / 29.1; ROCmFP4 T 128 21.4 / 26.5,
+// T 256 39.4 / 26.7; Q4_K T 128 25.9 / 41.5, T 256 47.5 / 41.9, T 2,427 387 / 55.6.
+static bool dense_mfma_faster(int type, size_t row_bytes, int N, int K, int T) {
+    const double items = (double)(N / 128) * ((T + 63) / 64), rounds = items <= 768 ? 1.0 : items / 768.0;
+    const double t_mfma = K / 128 * 1.8 * rounds;
+    const double bw = type == QT_Q8_0 ? 18e6 : type == QT_Q4_K ? 9.5e6 : 6e6;  // bytes per us
+    const double t_mv = (double)T * N * (double)row_bytes / bw;
+    return t_mfma < t_mv;
+}
+
+static std::atomic<int> g_dense_mode{0};
+extern "C" void qmatvec_dense_mfma_mode(int mode) { g_dense_mode.store(mode, std::memory_order_relaxed); }
 
 extern "C" hipError_t qmatvec_launch_q8_batch(int type, const void* W, size_t row_bytes, const qmatvec_q8* q, float* y,
                                               long long ldy, int N, int K, int T, hipStream_t stream) {
     const uint8_t *v = nullptr, *s = nullptr;
     long long vgs = 0, sgs = 0;
-    if (T >= DENSE_MFMA_MIN_T && N > 0 && ldy >= N && y && check_common(type, W, row_bytes, q, K, T) == hipSuccess &&
-        moe_grouped_mfma_ok(type, N, K) && find_tiles(W, type, K, row_bytes, &v, &s, &vgs, &sgs))
+    const int mode = g_dense_mode.load(std::memory_order_relaxed);
+    if (T >= 8 && mode != 2 && N > 0 && ldy >= N && y && check_common(type, W, row_bytes, q, K, T) == hipSuccess &&
+        moe_grouped_mfma_ok(type, N, K) && (mode == 1 || dense_mfma_faster(type, row_bytes, N, K, T)) &&
+        find_tiles(W, type, K, row_bytes, &v, &s, &vgs, &sgs))
         return moe_launch_dense_mfma(type, v, s, vgs, sgs, q, y, ldy, N, K, T, stream);
     return dense(type, W, N, y, nullptr, 0, nullptr, row_bytes, q, K, T, ldy, stream);
 }

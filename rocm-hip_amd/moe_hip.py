@@ -79,6 +79,7 @@ SIGNATURES = {
     "moe_layer_forward_norm": (_I, [ctypes.c_void_p, _P, _P, _P, _P, _F, _P, _I, _P, _P, _P, _P, _Z, _P]),
     "moe_layer_forward_noalloc": (_I, [ctypes.c_void_p, _P, _P, _I, _P, _P, _P, _P]),
     "moe_layer_set_fused": (None, [_I]),
+    "qmatvec_dense_mfma_mode": (None, [_I]),
     "moe_layer_fused_stamps": (None, [_P]),
     "moe_layer_fused_multi_q4k": (None, [_I]),
     # include/gguf_mmap.h (host only: the file mapping)

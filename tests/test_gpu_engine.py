@@ -2,7 +2,8 @@
 FFN sublayer issued launcher by launcher as the reference's QwenModel::moe_ffn / moe_core / moe_core_one do
 (src/qwen_model.cpp:839-937), on this library. Per T (1: the shared expert as a slot; 3: per-token launches; 40:
 the grouped launches): the residual x + proj bit-exact; the MoE output equal bit for bit to moe_layer_forward_norm
-on the same inputs (the layer entry point's fused kernels give the per-operation bits) and within the decode /
+on the same inputs (the layer entry point's fused kernels give the per-operation bits; the shared expert's dense
+launches held to the MFMA kernel, and within 1e-6 of those bits on the default kernel choice) and within the decode /
 prefill tolerance of the oracle; the next residual and norm consistent."""
 import ctypes
 
@@ -66,8 +67,14 @@ def test_engine_moe_ffn(moe, oracle, spec, packed):
             proj = rng.standard_normal((T, spec.E)).astype(np.float32)
             xd, pd, w1d, w2d = dev(x), dev(proj), dev(w1), dev(w2)
             x_mid, out, x_next, xn_next = (zeros((T, spec.E), torch.float32) for _ in range(4))
-            assert eng.moe_engine_ffn(e, ctypes.byref(el), cvoid(xd), cvoid(pd), cvoid(w1d), cvoid(w2d), EPS, T,
-                                      cvoid(x_mid), cvoid(out), cvoid(x_next), cvoid(xn_next), S()) == 0
+            # (the shared expert's dense launches on the MFMA kernel, as the layer entry point's merged tiles: the
+            # same bits; the default choice, checked below, may take the matvec kernel at small T)
+            moe.lib.qmatvec_dense_mfma_mode(1)
+            try:
+                assert eng.moe_engine_ffn(e, ctypes.byref(el), cvoid(xd), cvoid(pd), cvoid(w1d), cvoid(w2d), EPS, T,
+                                          cvoid(x_mid), cvoid(out), cvoid(x_next), cvoid(xn_next), S()) == 0
+            finally:
+                moe.lib.qmatvec_dense_mfma_mode(0)
             g_mid, g_out, g_next, g_xn = (host(t) for t in (x_mid, out, x_next, xn_next))
             # the layer entry point on the same sublayer input
             nb = moe.lib.moe_layer_scratch_bytes(ctypes.byref(desc), T)
@@ -81,6 +88,11 @@ def test_engine_moe_ffn(moe, oracle, spec, packed):
             assert np.array_equal(g_mid.view(np.uint32), r_mid.view(np.uint32)), T
             assert np.array_equal(g_out.view(np.uint32), r_out.view(np.uint32)), T
             assert np.array_equal(g_next.view(np.uint32), (g_mid + g_out).view(np.uint32)), T
+            if T >= 8:  # the default kernel choice for the dense launches: within fp32 reordering of those bits
+                out0 = zeros((T, spec.E), torch.float32)
+                assert eng.moe_engine_ffn(e, ctypes.byref(el), cvoid(xd), cvoid(pd), cvoid(w1d), cvoid(w2d), EPS, T,
+                                          cvoid(x_mid), cvoid(out0), cvoid(x_next), cvoid(xn_next), S()) == 0
+                assert rel_l2(host(out0), r_out) < 1e-6, T
             # the oracle on a few rows: RMSNorm, router logits, layer
             rows = np.arange(T) if T < 8 else rng.choice(T, 6, replace=False)
             y = np.stack([oracle.rmsnorm(g_mid[r], w1, EPS) for r in rows])
