@@ -164,7 +164,8 @@ __global__ void __launch_bounds__(256) k_combine(const float* down, const float*
 
 // One row per workgroup: x_out = x_in + add; y = x_out / sqrt(mean(x_out^2) + eps) * w, quantized per 256
 __global__ void __launch_bounds__(256) k_add_rmsnorm(const float* x_in, const float* add, float* x_out,
-                                                     const float* w, float* y, int n, float eps, Q8Out o) {
+                                                     const float* w, float* y, int n, float eps, Q8Out o,
+                                                     int wave_blocks) {
     __shared__ Q8Smem sh;
     __shared__ float part[4];
     const int t = threadIdx.x, row = blockIdx.x;
@@ -176,6 +177,31 @@ __global__ void __launch_bounds__(256) k_add_rmsnorm(const float* x_in, const fl
     const bool kept = n <= 256 * KEEP;
     float inv;
     float wn[KEEP];  // kept rows: the weights, loaded with x and add
+    if (kept && rms_rows4(xr, ar, n) && n % 256 == 0 && wave_blocks) {
+        // rms_first_pass4's layout is already the wave quantizer's: thread t's piece k is values 4 (t % 64) .. + 3 of
+        // 256-value block 4 k + t / 64, so each wave takes its blocks from registers (16-byte stores, no LDS)
+        const int lane = t & 63, wv = t >> 6, nb4 = n / 256;
+        float4 wq[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            wq[k] = w ? ((const float4*)w)[min(t + 256 * k, n / 4 - 1)] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        float4 keep4[4];
+        inv = rms_first_pass4(xr, ar, n, eps, keep4, part);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int b = 4 * k + wv;
+            if (b >= nb4) break;  // (uniform per wave)
+            const long long i = (long long)row * n + 256 * b + 4 * lane;
+            const float4 xv = keep4[k];
+            const float v[4] = {xv.x * inv * wq[k].x, xv.y * inv * wq[k].y, xv.z * inv * wq[k].z, xv.w * inv * wq[k].w};
+            if (ar) *(float4*)(x_out + i) = xv;
+            *(float4*)(y + i) = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) half_copy(o, i + j, v[j]);
+            q8_quantize_256_wave(v, (long long)row * nb4 + b, lane, o);
+        }
+        return;
+    }
     if (kept && rms_rows4(xr, ar, n)) {
         // the squares in the 16-byte layout (rms_first_pass4, shared with the fused layer), then the values moved
         // through LDS into this kernel's layout (t + 256 k: one per thread and 256-value block for the quantizer)
@@ -445,7 +471,11 @@ extern "C" hipError_t gpu_add_rmsnorm(const float* x_in, const float* add, float
     if (!moe_lib_ready()) return hipErrorNotInitialized;
     if (T <= 0 || n <= 0 || (q8 && (n % 256 != 0 || (long long)n * T > q8->max_k)) || (add && x_out == x_in))
         return hipErrorInvalidValue;
-    return launch_kernel(k_add_rmsnorm, dim3(T), dim3(256), 0, stream, x_in, add, x_out, w, y, n, eps, q8_out(q8));
+    // whole 256-value blocks on the wave quantizer where every row and output is aligned for its 16 / 4-byte stores
+    const int wave_blocks = n % 256 == 0 && aligned(y, 16) && (!add || aligned(x_out, 16)) && (!w || aligned(w, 16)) &&
+                            (!q8 || (aligned(q8->q0, 4) && aligned(q8->qK, 4)));
+    return launch_kernel(k_add_rmsnorm, dim3(T), dim3(256), 0, stream, x_in, add, x_out, w, y, n, eps, q8_out(q8),
+                         wave_blocks);
 }
 
 extern "C" hipError_t gpu_swiglu(const float* g, const float* u, float* out, int n, const qmatvec_q8* q8,
