@@ -6,7 +6,7 @@ GPU's fp32 gate / up sums, ~1e-7 from the oracle's double ones, may give the nei
 be within 1e-3; for the grouped prefill (T >= 8: dispatch, the MFMA or per-entry expert kernels, the shared expert
 as tiles or dense) 1e-3. The shapes are drawn from the ranges the launchers take (E and FE multiples of 256, up to
 128 experts, top-1 to top-8, with and without a shared expert), so the paths' selection rules meet shapes no fixed
-test has.
+test has. Decode outputs also equal the per-operation launches' bit for bit.
 """
 import numpy as np
 import pytest
@@ -81,3 +81,11 @@ def test_layer_sweep(moe, oracle, qtype, E, FE, NE, NU, shared, T, packed):
         err = rel_l2(got[t], want[k])
         if err >= 1e-5:
             assert err < 1e-3 and _quant_near_tie(oracle, spec, L, x[t], wids[k]), (t, err)
+    # the per-operation launches give the same bits as whatever decode path ran (fused or not)
+    moe.lib.moe_layer_set_fused(0)
+    try:
+        ref, rids, rwts = _run_layer(moe, spec, L, x, logits=logits, packed=packed)
+    finally:
+        moe.lib.moe_layer_set_fused(1)
+    assert np.array_equal(ids, rids) and np.array_equal(wts, rwts)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
