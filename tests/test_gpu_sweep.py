@@ -14,6 +14,7 @@ import pytest
 import synth
 from gpu_util import announce, rel_l2
 from test_gpu_parity import _run_layer
+from test_gpu_parity import test_layer_forward_norm_equals_add_rmsnorm_then_layer as _norm_case
 
 pytestmark = pytest.mark.gpu
 Q8_0, FP4, FAST, Q4_K = 8, 100, 101, 12
@@ -89,3 +90,14 @@ def test_layer_sweep(moe, oracle, qtype, E, FE, NE, NU, shared, T, packed):
         moe.lib.moe_layer_set_fused(1)
     assert np.array_equal(ids, rids) and np.array_equal(wts, rwts)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+NORM_SWEEP = [(synth.LayerSpec(c[0], c[1], c[3], c[4], c[2], c[5]), c[6], bool(i % 2), bool(i % 3))
+              for i, c in enumerate(CASES[:24])]
+
+
+@pytest.mark.parametrize("spec,T,with_add,with_w", NORM_SWEEP, ids=lambda v: str(getattr(v, "qtype", v)))
+def test_norm_layer_sweep(moe, spec, T, with_add, with_w):
+    """The sweep's first 24 shapes through moe_layer_forward_norm (the RMSNorm producer fused into the layer's first
+    kernel where the fused path takes the layer): the bits of gpu_add_rmsnorm followed by moe_layer_forward."""
+    _norm_case(moe, spec, T, with_add, with_w)
