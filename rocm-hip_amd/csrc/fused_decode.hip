@@ -54,7 +54,7 @@ __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
     if (pre || pre_gate)
 #pragma unroll
         for (int k = 0; k < FD_MAX_E / 1024; ++k)
-            if (tid + 256 * k < E / 4) wpre[k] = ((const float4*)(pre ? wrow : a.w_shexp))[tid + 256 * k];
+            if (tid + 256 * k < E / 4) wpre[k] = ld_w4((const float4*)(pre ? wrow : a.w_shexp) + tid + 256 * k);
     if (a.norm && rms_rows4(a.x, a.add, E)) {
         // every workgroup forms the normalized input itself (E <= 4096 values, from L2) in the 16-byte layout of the
         // router-row dot (rms_first_pass4): a router workgroup dots it in place, with f32_row_dot's order; the

@@ -123,13 +123,22 @@ __device__ __forceinline__ void acc_block(v16f& acc, const v16i& I, const v16f& 
 // lane. The FP4 kernel stages its activations through registers instead (converted to FP16 on the way). The weight
 // rows' scales come through registers.
 typedef __attribute__((address_space(3))) void lds_void;
+#ifndef GG_WNT
+#define GG_WNT 0  // cache policy bits of the weight tiles' LDS-direct loads (2, nontemporal, measured slower: config 4
+                  // layer prefill 0.44 -> 0.48 ms, config 3 1.30 -> 1.41 -- the tiles of an expert's row block are
+                  // re-read by each of its entry tiles, from L2)
+#endif
 
 __device__ __forceinline__ void lds_load16(const void* g, void* lds_run) {
     __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_run, 16, 0, 0);
 }
 // 12 bytes a lane: they land in 16-byte LDS slots (lane l at 16 l)
 __device__ __forceinline__ void lds_load12(const void* g, void* lds_run) {
-    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_run, 12, 0, 0);
+    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_run, 12, 0, GG_WNT);
+}
+// The weight tiles' 16-byte loads (the cache policy GG_WNT)
+__device__ __forceinline__ void lds_load16w(const void* g, void* lds_run) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_run, 16, 0, GG_WNT);
 }
 
 template <int WAITS>
@@ -192,7 +201,7 @@ __device__ __forceinline__ void q_issue(GBuf<QT_Q8_0, NM, KB>& B, int b0, uint4 
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int c = 0; c < KB; ++c) lds_load16(vt[m] + 1024 * (b0 + c), B.a[m][w][c]);
+        for (int c = 0; c < KB; ++c) lds_load16w(vt[m] + 1024 * (b0 + c), B.a[m][w][c]);
 #pragma unroll
     for (int j = 0; j < KB * GG_NT / 4; ++j) {
         const int bb = w / GG_NT + (4 / GG_NT) * j;

@@ -26,7 +26,7 @@ __device__ __forceinline__ float f32_row_dot(const float* wr, const float* x, in
         const float4* x4 = (const float4*)x;
 #pragma unroll 4
         for (int i = tid; i < K / 4; i += 256) {
-            const float4 a = w4[i], b = x4[i];
+            const float4 a = ld_w4(w4 + i), b = x4[i];
             acc = fmaf(a.x, b.x, acc);
             acc = fmaf(a.y, b.y, acc);
             acc = fmaf(a.z, b.z, acc);
@@ -51,7 +51,7 @@ __device__ __forceinline__ void f32_row_dot_multi(const float* wr, const float* 
     if (vec) {
         const float4* w4 = (const float4*)wr;
         for (int i = tid; i < K / 4; i += 256) {
-            const float4 a = w4[i];
+            const float4 a = ld_w4(w4 + i);
             float4 b[TMAX];
 #pragma unroll
             for (int t = 0; t < TMAX; ++t) b[t] = ((const float4*)(x + (size_t)min(t, T - 1) * ldx))[i];
@@ -89,7 +89,7 @@ __device__ __forceinline__ float shexp_gate(const float* xr, const float* w, int
     float d = 0.0f;
     if ((n & 3) == 0 && (((uintptr_t)xr | (uintptr_t)w) & 15) == 0) {
         for (int i = tid; i < n / 4; i += 256) {
-            const float4 a = ((const float4*)xr)[i], b = ((const float4*)w)[i];
+            const float4 a = ((const float4*)xr)[i], b = ld_w4((const float4*)w + i);
             d += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
         }
     } else {
