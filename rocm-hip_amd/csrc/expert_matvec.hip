@@ -43,7 +43,9 @@ __device__ __forceinline__ void act_row(const MvArgs& a, long long in_row, const
 }
 
 // grid (row blocks, n_used * (1 or 2) slots, T tokens) in id mode; (row blocks, 1 or 2 matrices, T) dense
-template <int TYPE, bool PACKED, int L, int R, int NUPL>
+// NT: the weights as nontemporal loads (each row read once per launch: decode, one token or the id launches); the
+// dense batches of several tokens re-read the matrix per token from L2 and take ordinary loads
+template <int TYPE, bool PACKED, int L, int R, int NUPL, bool NT>
 __global__ void __launch_bounds__(256) k_expert_mv(MvArgs a) {
     constexpr int G = 64 / L;  // row groups per wave
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -75,7 +77,7 @@ __global__ void __launch_bounds__(256) k_expert_mv(MvArgs a) {
     const int* xbs;
     act_row<TYPE>(a, in_row, xq, xd, xbs);
     float acc[R];
-    rows_dot<TYPE, PACKED, L, R, NUPL>(vbase, sbase, a.vrb, a.srb, row0, G, nrows, xq, xd, xbs, a.K, gl, acc);
+    rows_dot<TYPE, PACKED, L, R, NUPL>(vbase, sbase, a.vrb, a.srb, row0, G, nrows, xq, xd, xbs, a.K, gl, acc, NT);
     if (gl == 0) {
         float* y = (mi & 1 ? a.y2 : a.y) + out_row * a.ldy;
 #pragma unroll
@@ -107,7 +109,8 @@ __global__ void __launch_bounds__(256) k_expert_entries(MvArgs a, const int* n_t
         const int* xbs;
         act_row<TYPE>(a, in_rows[st + i], xq, xd, xbs);
         float acc[R];
-        rows_dot<TYPE, PACKED, L, R, 0>(vbase, sbase, a.vrb, a.srb, row0, G, a.N, xq, xd, xbs, a.K, gl, acc);
+        rows_dot<TYPE, PACKED, L, R, 0>(vbase, sbase, a.vrb, a.srb, row0, G, a.N, xq, xd, xbs, a.K, gl, acc,
+                                        false);  // (the rows are re-read per entry: ordinary loads keep them in L2)
         if (gl == 0) {
             float* y = a.y + (long long)out_rows[st + i] * a.N;
 #pragma unroll
@@ -372,7 +375,8 @@ hipError_t launch_mv_l(const MvArgs& a, dim3 yz, int nrows, hipStream_t st) {
     constexpr int R = rows_in_flight(L, NUPL);
     const int rpb = 4 * R * (64 / L);
     const dim3 g((nrows + rpb - 1) / rpb, yz.y, yz.z), b(256);
-    return launch_kernel(k_expert_mv<TYPE, PACKED, L, R, NUPL>, g, b, 0, st, a);
+    if (a.ids || yz.z == 1) return launch_kernel(k_expert_mv<TYPE, PACKED, L, R, NUPL, true>, g, b, 0, st, a);
+    return launch_kernel(k_expert_mv<TYPE, PACKED, L, R, NUPL, false>, g, b, 0, st, a);
 }
 
 template <int TYPE, bool PACKED, int L>

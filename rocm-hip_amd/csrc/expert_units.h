@@ -67,14 +67,13 @@ __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return *(const ui
 #ifndef EU_NT_S
 #define EU_NT_S 1
 #endif
-__device__ __forceinline__ uint32_t ld_s16(const uint8_t* p) {
+__device__ __forceinline__ uint32_t ld_s16(const uint8_t* p, bool nt = true) {
 #if EU_NT_S
-    return __builtin_nontemporal_load((const uint16_t*)p);
-#else
-    return *(const uint16_t*)p;
+    if (nt) return __builtin_nontemporal_load((const uint16_t*)p);
 #endif
-}
-__device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) { return *(const uint32_t*)p; }
+    (void)nt;
+    return *(const uint16_t*)p;
+}__device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) { return *(const uint32_t*)p; }
 // The 16-byte weight loads of the row dots as nontemporal loads (each weight byte is read once per launch). Measured
 // per decode layer (us): config 1 17.4-17.9 -> 16.7, config 0 18.8 -> 17.7, config 3 22.5 -> 21.8, config 3 at
 // T = 4 54.6 -> 52.3; config 4's 40-layer stack 1,430 -> 1,517 tokens/s.
@@ -82,15 +81,16 @@ __device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) { return *(const ui
 #define EU_NT 1
 #endif
 typedef unsigned int eu_v4u __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 ld_u128(const uint8_t* p) {
+__device__ __forceinline__ uint4 ld_u128(const uint8_t* p, bool nt = true) {
 #if EU_NT
-    const eu_v4u v = __builtin_nontemporal_load((const eu_v4u*)p);
-    return make_uint4(v.x, v.y, v.z, v.w);
-#else
-    return *(const uint4*)p;
+    if (nt) {
+        const eu_v4u v = __builtin_nontemporal_load((const eu_v4u*)p);
+        return make_uint4(v.x, v.y, v.z, v.w);
+    }
 #endif
+    (void)nt;
+    return *(const uint4*)p;
 }
-
 // ---- native GGUF rows (row pointer 4-byte aligned, as the reference's launchers require)
 template <int TYPE>
 __device__ __forceinline__ void load_native(const uint8_t* row, int u, WUnit<TYPE>& w);
@@ -130,35 +130,36 @@ __device__ __forceinline__ void load_native<QT_Q4_K>(const uint8_t* row, int u, 
 
 // ---- split-plane rows: vrow / srow point at the row in the value / scale plane; nu = units per row
 template <int TYPE>
-__device__ __forceinline__ void load_packed(const uint8_t* vrow, const uint8_t* srow, int u, int nu, WUnit<TYPE>& w);
+__device__ __forceinline__ void load_packed(const uint8_t* vrow, const uint8_t* srow, int u, int nu, WUnit<TYPE>& w,
+                                            bool nt = true);
 
 template <>
 __device__ __forceinline__ void load_packed<QT_Q8_0>(const uint8_t* vrow, const uint8_t* srow, int u, int nu,
-                                                     WUnit<QT_Q8_0>& w) {
-    const uint4 a = ld_u128(vrow + 16 * u), b = ld_u128(vrow + 16 * (nu + u));
+                                                     WUnit<QT_Q8_0>& w, bool nt) {
+    const uint4 a = ld_u128(vrow + 16 * u, nt), b = ld_u128(vrow + 16 * (nu + u), nt);
     w.q[0] = a.x, w.q[1] = a.y, w.q[2] = a.z, w.q[3] = a.w;
     w.q[4] = b.x, w.q[5] = b.y, w.q[6] = b.z, w.q[7] = b.w;
-    w.s[0] = ld_s16(srow + 2 * u);
+    w.s[0] = ld_s16(srow + 2 * u, nt);
 }
 template <>
 __device__ __forceinline__ void load_packed<QT_ROCMFP4>(const uint8_t* vrow, const uint8_t* srow, int u, int nu,
-                                                        WUnit<QT_ROCMFP4>& w) {
-    const uint4 a = ld_u128(vrow + 16 * u);
+                                                        WUnit<QT_ROCMFP4>& w, bool nt) {
+    const uint4 a = ld_u128(vrow + 16 * u, nt);
     w.q[0] = a.x, w.q[1] = a.y, w.q[2] = a.z, w.q[3] = a.w;
-    w.s[0] = ld_s16(srow + 2 * u);
+    w.s[0] = ld_s16(srow + 2 * u, nt);
 }
 template <>
 __device__ __forceinline__ void load_packed<QT_ROCMFP4_FAST>(const uint8_t* vrow, const uint8_t* srow, int u, int nu,
-                                                             WUnit<QT_ROCMFP4_FAST>& w) {
-    const uint4 a = ld_u128(vrow + 16 * u);
+                                                             WUnit<QT_ROCMFP4_FAST>& w, bool nt) {
+    const uint4 a = ld_u128(vrow + 16 * u, nt);
     w.q[0] = a.x, w.q[1] = a.y, w.q[2] = a.z, w.q[3] = a.w;
     w.s[0] = srow[u];
 }
 template <>
 __device__ __forceinline__ void load_packed<QT_Q4_K>(const uint8_t* vrow, const uint8_t* srow, int u, int nu,
-                                                     WUnit<QT_Q4_K>& w) {
-    const uint4 a = ld_u128(vrow + 16 * u), b = ld_u128(vrow + 16 * (nu + u));
-    const uint4 h = ld_u128(srow + 16 * (u >> 2));
+                                                     WUnit<QT_Q4_K>& w, bool nt) {
+    const uint4 a = ld_u128(vrow + 16 * u, nt), b = ld_u128(vrow + 16 * (nu + u), nt);
+    const uint4 h = ld_u128(srow + 16 * (u >> 2), nt);
     w.q[0] = a.x, w.q[1] = a.y, w.q[2] = a.z, w.q[3] = a.w;
     w.q[4] = b.x, w.q[5] = b.y, w.q[6] = b.z, w.q[7] = b.w;
     w.s[0] = h.x, w.s[1] = h.y, w.s[2] = h.z, w.s[3] = h.w;
@@ -254,9 +255,10 @@ __device__ __forceinline__ float term(const WUnit<TYPE>& w, const XUnit<TYPE>& x
 }
 
 template <int TYPE, bool PACKED>
-__device__ __forceinline__ void load_unit(const uint8_t* vrow, const uint8_t* srow, int u, int nu, WUnit<TYPE>& w) {
+__device__ __forceinline__ void load_unit(const uint8_t* vrow, const uint8_t* srow, int u, int nu, WUnit<TYPE>& w,
+                                          bool nt = true) {
     if constexpr (PACKED)
-        load_packed<TYPE>(vrow, srow, u, nu, w);
+        load_packed<TYPE>(vrow, srow, u, nu, w, nt);
     else
         load_native<TYPE>(vrow, u, w);
 }
@@ -267,7 +269,7 @@ __device__ __forceinline__ void load_unit(const uint8_t* vrow, const uint8_t* sr
 template <int TYPE, bool PACKED, int L, int R, int NUPL>
 __device__ __forceinline__ void rows_dot(const uint8_t* vbase, const uint8_t* sbase, long long vrb, long long srb,
                                          int row0, int stride, int nrows, const int8_t* xq, const float* xd,
-                                         const int* xbs, int K, int gl, float acc[R]) {
+                                         const int* xbs, int K, int gl, float acc[R], bool nt = true) {
     const int nu = fmt_units(TYPE, K);
     const uint8_t* vr[R];
     const uint8_t* sr[R];
@@ -284,7 +286,7 @@ __device__ __forceinline__ void rows_dot(const uint8_t* vbase, const uint8_t* sb
 #pragma unroll
         for (int i = 0; i < NUPL; ++i)
 #pragma unroll
-            for (int r = 0; r < R; ++r) load_unit<TYPE, PACKED>(vr[r], sr[r], gl + i * L, nu, w[i][r]);
+            for (int r = 0; r < R; ++r) load_unit<TYPE, PACKED>(vr[r], sr[r], gl + i * L, nu, w[i][r], nt);
 #pragma unroll
         for (int i = 0; i < NUPL; ++i) load_x<TYPE>(xq, xd, xbs, gl + i * L, x[i]);
 #pragma unroll
@@ -297,7 +299,7 @@ __device__ __forceinline__ void rows_dot(const uint8_t* vbase, const uint8_t* sb
             load_x<TYPE>(xq, xd, xbs, u, x);
             WUnit<TYPE> w[R];
 #pragma unroll
-            for (int r = 0; r < R; ++r) load_unit<TYPE, PACKED>(vr[r], sr[r], u, nu, w[r]);
+            for (int r = 0; r < R; ++r) load_unit<TYPE, PACKED>(vr[r], sr[r], u, nu, w[r], nt);
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[r] += term<TYPE>(w[r], x, u);
         }
