@@ -17,6 +17,15 @@ struct qmatvec_q8;
 hipError_t moe_swiglu_q8(const float* g, const float* u, float* out, int n, const qmatvec_q8* q8, hipStream_t stream,
                          int parts);
 
+// gpu_moe_router that also quantizes x [T][n] into q8 (formats as in moe_swiglu_q8's parts); gpu_add_rmsnorm that
+// also quantizes y. Both return hipErrorInvalidValue where their conditions (n % 256 == 0, alignment; the norm:
+// n <= 4096) do not hold, and the caller then launches the quantizer on its own.
+hipError_t moe_router_quantize(const float* logits, const float* x, const float* w_shexp, int* ids, float* wts,
+                               float* sg, int n_expert, int n_used, int n, int T, int ids_stride, const qmatvec_q8* q8,
+                               int parts, hipStream_t stream);
+hipError_t moe_add_rmsnorm_q8(const float* x_in, const float* add, float* x_out, const float* w, float* y, int n,
+                              int T, float eps, const qmatvec_q8* q8, int parts, hipStream_t stream);
+
 template <typename T>
 struct same_type {
     typedef T type;

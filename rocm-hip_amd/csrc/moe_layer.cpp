@@ -119,9 +119,10 @@ extern "C" size_t moe_layer_scratch_bytes(const moe_layer_desc* d, int max_t) {
     return plan(d, max_t).total;
 }
 
-extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x, const float* logits_in, int T,
-                                        float* out, int* ids_out, float* wts_out, void* scratch, size_t scratch_bytes,
-                                        hipStream_t st) {
+// xq: x's quantized bundle is already in the plan's qx (the producer wrote it; T >= 8 only)
+static hipError_t layer_forward(const moe_layer_desc* d, const float* x, const float* logits_in, int T, float* out,
+                                int* ids_out, float* wts_out, void* scratch, size_t scratch_bytes, hipStream_t st,
+                                bool xq) {
     if (!d || !x || !out || T <= 0 || !scratch || ((uintptr_t)scratch & 255)) return hipErrorInvalidValue;
     const Plan p = plan(d, T);
     if (scratch_bytes < p.total) return hipErrorInvalidValue;
@@ -157,7 +158,10 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
         lg = (float*)logits_in;
     else if (front)
         CHECK(qmatvec_launch_batch(0, d->w_router, (size_t)E * 4, x, lg, NE, E, T, st));
-    if (!front) {
+    // the prefill's router launch quantizes x as well (saving the quantizer's launch), unless the producer did
+    const bool fuse_q = T >= 8 && (pm & 1) && !xq && E % 256 == 0 && aligned(x, 16) && aligned(qx.q0, 4) &&
+                        aligned(qx.qK, 4);
+    if (!front || xq || fuse_q) {
     } else if (type == 12) {  // Q4_K reads Q8_K activations; the others read Q8_0 values and scales only
         CHECK(moe_quantize_q8k(x, T * E, &qx, st));
     } else {
@@ -186,7 +190,10 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
             CHECK(gpu_moe_combine(down, wts, nullptr, nullptr, out, NU, E, T, st));
         }
     } else {
-        if (pm & 1) CHECK(gpu_moe_router(lg, x, d->w_shexp, ids, wts, sg, NE, NU, E, T, st, NU));
+        if (fuse_q)
+            CHECK(moe_router_quantize(lg, x, d->w_shexp, ids, wts, sg, NE, NU, E, T, NU, &qx, type == 12 ? 2 : 1, st));
+        else if (pm & 1)
+            CHECK(gpu_moe_router(lg, x, d->w_shexp, ids, wts, sg, NE, NU, E, T, st, NU));
         int* tok = (int*)(s + p.tok);
         int* pair = (int*)(s + p.pair);
         int* ntile = (int*)(s + p.ntile);
@@ -260,6 +267,12 @@ extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x,
     return hipSuccess;
 }
 
+extern "C" hipError_t moe_layer_forward(const moe_layer_desc* d, const float* x, const float* logits_in, int T,
+                                        float* out, int* ids_out, float* wts_out, void* scratch, size_t scratch_bytes,
+                                        hipStream_t st) {
+    return layer_forward(d, x, logits_in, T, out, ids_out, wts_out, scratch, scratch_bytes, st, false);
+}
+
 // The producer fused in: y = RMSNorm(x_in + add) * w_norm, x_out = x_in + add, then the layer on y. T == 1 with the
 // fused decode kernels forms y inside their first kernel; every other case runs gpu_add_rmsnorm into scratch first.
 // Either way the results equal gpu_add_rmsnorm followed by moe_layer_forward bit for bit.
@@ -278,6 +291,13 @@ extern "C" hipError_t moe_layer_forward_norm(const moe_layer_desc* d, const floa
         if (moe_fused_try(d, x_in, logits, out, ids_out, wts_out, scratch, 7, st, &e, &nm)) return e;
     }
     float* y = (float*)((char*)scratch + p.ynorm);
+    if (T >= 8) {  // the prefill: the norm writes y's quantized bundle too, where its wave path applies
+        qmatvec_q8 qx;
+        qmatvec_q8_bind(&qx, (char*)scratch + p.qx, p.qx_k);
+        if (moe_add_rmsnorm_q8(x_in, add, x_out, w_norm, y, d->n_embd, T, eps, &qx, d->type == 12 ? 2 : 1, st) ==
+            hipSuccess)
+            return layer_forward(d, y, logits, T, out, ids_out, wts_out, scratch, scratch_bytes, st, true);
+    }
     CHECK(gpu_add_rmsnorm(x_in, add, x_out, w_norm, y, d->n_embd, T, eps, nullptr, st));
-    return moe_layer_forward(d, y, logits, T, out, ids_out, wts_out, scratch, scratch_bytes, st);
+    return layer_forward(d, y, logits, T, out, ids_out, wts_out, scratch, scratch_bytes, st, false);
 }

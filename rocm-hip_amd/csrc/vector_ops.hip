@@ -391,14 +391,26 @@ __global__ void __launch_bounds__(64 * MF_KS) k_matmul_f32_mfma(const float* W, 
 
 // ------------------------------------------------------------------ router (src/gpu_ops.hip:185-241)
 
-// One 256-thread workgroup per token: the shared-expert gate, then router_select (router_dev.h).
+// One 256-thread workgroup per token: the shared-expert gate, then router_select (router_dev.h). QX (the layer's
+// prefill): waves 1..3 also quantize the token's row of x (n % 256 == 0) into o while wave 0 selects -- the wave
+// quantizer's expressions, so the bits of k_quantize_q8_w / k_quantize_q8_0 -- which saves the quantizer's launch.
+template <bool QX>
 __global__ void __launch_bounds__(256) k_router(const float* logits, const float* x, const float* w_shexp, int* ids,
-                                                float* wts, float* sg, int ne, int nu, int n, int ids_stride) {
+                                                float* wts, float* sg, int ne, int nu, int n, int ids_stride, Q8Out o) {
     __shared__ float part[4];
     const int t = blockIdx.x, tid = threadIdx.x;
     if (w_shexp) {  // (uniform branch)
         const float g = shexp_gate(x + (size_t)t * n, w_shexp, n, part);
         if (tid == 0) sg[t] = g;
+    }
+    if (QX && tid >= 64) {
+        const int nb = n / 256, lane = tid & 63;
+        for (int b = (tid >> 6) - 1; b < nb; b += 3) {
+            const long long blk = (long long)t * nb + b;
+            const float4 p = *(const float4*)(x + blk * 256 + 4 * lane);
+            const float v[4] = {p.x, p.y, p.z, p.w};
+            q8_quantize_256_wave(v, blk, lane, o);
+        }
     }
     int* id_row = ids + (size_t)t * ids_stride;
     router_select(logits + (size_t)t * ne, ne, nu, id_row, wts + (size_t)t * nu);
@@ -510,8 +522,38 @@ extern "C" hipError_t gpu_moe_router(const float* logits, const float* x, const 
         return hipErrorInvalidValue;
     if (ids_stride == 0) ids_stride = n_used;
     if (ids_stride < n_used || (w_shexp && (!x || !sg || n <= 0))) return hipErrorInvalidValue;
-    return launch_kernel(k_router, dim3(T), dim3(256), 0, stream, logits, x, w_shexp, ids, wts, sg, n_expert, n_used,
-                         n, ids_stride);
+    return launch_kernel(k_router<false>, dim3(T), dim3(256), 0, stream, logits, x, w_shexp, ids, wts, sg, n_expert,
+                         n_used, n, ids_stride, Q8Out{});
+}
+
+// Internal (moe_layer_forward): gpu_moe_router with x [T][n] quantized into q8 (the formats in parts) by the same
+// launch; n % 256 == 0, x 16-byte and the values 4-byte aligned
+hipError_t moe_router_quantize(const float* logits, const float* x, const float* w_shexp, int* ids, float* wts,
+                               float* sg, int n_expert, int n_used, int n, int T, int ids_stride, const qmatvec_q8* q8,
+                               int parts, hipStream_t stream) {
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (n_expert <= 0 || n_expert > 1024 || n_used <= 0 || n_used > 64 || n_used > n_expert || T <= 0 || n <= 0 ||
+        n % 256 || !x || !q8 || q8->xh || (long long)n * T > q8->max_k || !aligned(x, 16) || !aligned(q8->q0, 4) ||
+        !aligned(q8->qK, 4))
+        return hipErrorInvalidValue;
+    if (ids_stride == 0) ids_stride = n_used;
+    if (ids_stride < n_used || (w_shexp && !sg)) return hipErrorInvalidValue;
+    return launch_kernel(k_router<true>, dim3(T), dim3(256), 0, stream, logits, x, w_shexp, ids, wts, sg, n_expert,
+                         n_used, n, ids_stride, q8_out_parts(q8, parts));
+}
+
+// Internal (moe_layer_forward_norm): gpu_add_rmsnorm with y's quantized bundle (the formats in parts) written by the
+// same launch, on its wave path only (rows of at most 4,096 values, a multiple of 256, every row and output
+// aligned), which returns hipErrorInvalidValue where that path does not apply
+hipError_t moe_add_rmsnorm_q8(const float* x_in, const float* add, float* x_out, const float* w, float* y, int n,
+                              int T, float eps, const qmatvec_q8* q8, int parts, hipStream_t stream) {
+    if (!moe_lib_ready()) return hipErrorNotInitialized;
+    if (T <= 0 || n <= 0 || n > 4096 || n % 256 || !q8 || q8->xh || (long long)n * T > q8->max_k ||
+        (add && x_out == x_in) || !aligned(x_in, 16) || (add && !aligned(add, 16)) || !aligned(y, 16) ||
+        (add && !aligned(x_out, 16)) || (w && !aligned(w, 16)) || !aligned(q8->q0, 4) || !aligned(q8->qK, 4))
+        return hipErrorInvalidValue;
+    return launch_kernel(k_add_rmsnorm, dim3(T), dim3(256), 0, stream, x_in, add, x_out, w, y, n, eps,
+                         q8_out_parts(q8, parts), 1);
 }
 
 extern "C" hipError_t gpu_moe_combine_scaled(const float* down, const float* wts, const float* shared, const float* sg,
