@@ -57,7 +57,7 @@ __global__ void __launch_bounds__(256) k_expert_mv(MvArgs a) {
     if (a.ids) {
         const bool m2 = (int)blockIdx.y >= a.n_used;
         slot = blockIdx.y - (m2 ? a.n_used : 0);
-        e = a.ids[(long long)t * a.n_used + slot];
+        e = wave_uniform(a.ids[(long long)t * a.n_used + slot]);
         mi = (e >= 0 ? 0 : 2) + (m2 ? 1 : 0);
         out_row = (long long)t * a.n_used + slot;
     } else {

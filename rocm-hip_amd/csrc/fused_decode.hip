@@ -221,8 +221,8 @@ __global__ void __launch_bounds__(64 * (64 / FD_GU_RW)) k_fd_gate_up(FArgs a) {
         }
     }
     stamp(a, 3);
-    const int e = slot < NU ? s_ids[slot] : -1;
-    const int mat = w / WPM;  // the first WPM waves: gate rows; the next WPM: up rows
+    const int e = wave_uniform(slot < NU ? s_ids[slot] : -1);
+    const int mat = wave_uniform(w / WPM);  // the first WPM waves: gate rows; the next WPM: up rows
     const int mi = e >= 0 ? mat : 3 + mat;
     const long long rbase = e >= 0 ? (long long)e * FE : 0;
     const uint8_t* vb = pick(a.v, mi) + rbase * a.vrb_in;
@@ -265,7 +265,7 @@ __global__ void __launch_bounds__(1024) k_fd_down(FArgs a) {
     stamp(a, 5);
     const float sgv = a.has_gate && tid < RB ? a.sg[t] : 0.0f;  // (read now: kernel 1 wrote it)
     if (slot < NS) {
-        const int e = slot < NU ? a.ids[t * a.ids_ld + slot] : -1;
+        const int e = wave_uniform(slot < NU ? a.ids[t * a.ids_ld + slot] : -1);
         const long long row = e >= 0 ? (long long)e * E + i0 + i : i0 + i;
         const int mi = e >= 0 ? 2 : 5;
         const uint8_t* vr[1] = {pick(a.v, mi) + row * a.vrb_out};
@@ -320,7 +320,7 @@ __global__ void __launch_bounds__(1024) k_fd_down_q8k(FArgs a) {
     stamp(a, 5);
     const float sgv = a.has_gate && tid < RB * RS ? a.sg[t] : 0.0f;  // (read now: kernel 1 wrote it)
     if (slot < NS) {
-        const int e = slot < NU ? a.ids[t * a.ids_ld + slot] : -1;
+        const int e = wave_uniform(slot < NU ? a.ids[t * a.ids_ld + slot] : -1);
         const int mi = e >= 0 ? 2 : 5;
         const long long rbase = e >= 0 ? (long long)e * E : 0;
         const uint8_t* vb = pick(a.v, mi) + rbase * a.vrb_out;

@@ -291,8 +291,8 @@ __global__ void __launch_bounds__(512) k_fm_gate_up_unit(FArgs a) {
     stamp(a, 3);
     const int u = blockIdx.x / nbf, b = blockIdx.x - u * nbf;
     if (u >= s_nu) return;  // (uniform) past the union's end
-    const int e = ulist[u];
-    const int mat = w / WPM, r0 = RW * (w % WPM) + grp * R;  // gate or up; this group's first row of the unit's 32
+    const int e = wave_uniform(ulist[u]);
+    const int mat = wave_uniform(w / WPM), r0 = RW * (w % WPM) + grp * R;  // gate or up; this group's first row
     {
         const int mi = e >= 0 ? mat : 3 + mat;
         const long long rbase = (e >= 0 ? (long long)e * FE : 0) + 32 * b + r0;

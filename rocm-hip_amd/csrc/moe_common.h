@@ -59,6 +59,11 @@ __device__ __forceinline__ T pick(const T (&p)[N], int i) {
     return r;
 }
 
+// A value every lane of the wave holds, moved to a scalar register: an index into the kernel's plane pointers made
+// wave-uniform this way is chosen by scalar selects or a scalar load of the argument, where a per-lane index had
+// compiled to a vector load from the kernel-argument segment ahead of every weight load
+__device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
 // pick for pointers where the optimizer folds pick's selects back into such a load (it did where i depends on a
 // value read from LDS, in the multi-token kernels): every element first passes, unconditionally, through an
 // empty asm statement that keeps it in scalar registers. (Not the default: it costs the T = 1 kernels ~0.7 µs.)
