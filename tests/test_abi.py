@@ -168,3 +168,13 @@ def test_registered_bytes_per_mode():
         assert lib.qmatvec_registered_bytes(t, rows, K, 2) == native
         assert lib.qmatvec_registered_bytes(t, rows, K, 3) == 0
     assert lib.qmatvec_registered_bytes(8, rows, K, 4) == 0 and lib.qmatvec_registered_bytes(2, rows, K, 0) == 0
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus above 1 exits at once with a message that says so (no GPU needed)."""
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr)
