@@ -29,11 +29,18 @@
 // entries past nu, and for a token past T). NM = 8, 16 or 64: the smallest that holds n_used (<= 64).
 // Returns the row's number of levels (largest occurrence index + 1; 0 for no valid entry). The loads are
 // unconditional within a live row: under a per-id branch each one had waited for the previous.
+// (row: a valid row even for a token past T -- the caller clamps it -- so that every load is unconditional: loads
+// under the live condition had compiled to branches that waited for each pair before issuing the next)
 template <int NM>
-__device__ __forceinline__ int group_row(const int* row, int nu, int ne, bool live, int (&pk)[NM]) {
-    int r[NM];
+__device__ __forceinline__ void group_row_load(const int* row, int nu, bool live, int (&r)[NM]) {
 #pragma unroll
-    for (int j = 0; j < NM; ++j) r[j] = live ? row[min(j, nu - 1)] : -1;
+    for (int j = 0; j < NM; ++j) {
+        const int v = row[min(j, nu - 1)];
+        r[j] = live ? v : -1;
+    }
+}
+template <int NM>
+__device__ __forceinline__ int group_row_keys(const int (&r)[NM], int nu, int ne, int (&pk)[NM]) {
     int lv = 0;
 #pragma unroll
     for (int j = 0; j < NM; ++j) {
@@ -45,6 +52,12 @@ __device__ __forceinline__ int group_row(const int* row, int nu, int ne, bool li
         lv = ok ? max(lv, occ + 1) : lv;
     }
     return lv;
+}
+template <int NM>
+__device__ __forceinline__ int group_row(const int* row, int nu, int ne, bool live, int (&pk)[NM]) {
+    int r[NM];
+    group_row_load<NM>(row, nu, live, r);
+    return group_row_keys<NM>(r, nu, ne, pk);
 }
 
 // The largest of the workgroup's lv (LDS word *slot, which the caller set to 0 before a barrier)
@@ -119,7 +132,7 @@ __global__ void __launch_bounds__(64 * GROUP_WAVES) k_moe_group(const int* ids, 
             __syncthreads();
             const int t = t0 + tid;
             int pk[NM], acc[NM];
-            const int levels = group_levels(group_row<NM>(ids + (size_t)t * nu, nu, ne, t < T, pk), &lvmax);
+            const int levels = group_levels(group_row<NM>(ids + (size_t)min(t, T - 1) * nu, nu, ne, t < T, pk), &lvmax);
 #pragma unroll
             for (int j = 0; j < NM; ++j) acc[j] = 0;
             for (int k = 0; k < levels; ++k) {
@@ -211,7 +224,7 @@ __global__ void __launch_bounds__(64 * GB_WAVES) k_group_count(const int* ids, i
     if (tid == 0) lvmax = 0;
     __syncthreads();
     int pk[NM];
-    const int levels = group_levels(group_row<NM>(ids + (size_t)t * nu, nu, ne, t < T, pk), &lvmax);
+    const int levels = group_levels(group_row<NM>(ids + (size_t)min(t, T - 1) * nu, nu, ne, t < T, pk), &lvmax);
     for (int k = 0; k < levels; ++k) group_level<GB_WAVES, NM>(pk, k, ne, masks, pre, bc);
     for (int e = tid; e < ne; e += 64 * GB_WAVES) ws[(size_t)blockIdx.x * ne + e] = bc[e];
 }
@@ -262,12 +275,22 @@ __global__ void __launch_bounds__(64 * GB_WAVES) k_group_place(const int* ids, i
     __shared__ int part[4];
     __shared__ int lvmax;
     const int tid = threadIdx.x, t = blockIdx.x * 64 * GB_WAVES + tid;
+    // this thread's row of ids loaded first: those loads fly with the count table's
+    int r[NM];
+    group_row_load<NM>(ids + (size_t)min(t, T - 1) * nu, nu, t < T, r);
+    if (tid == 0) lvmax = 0;  // (visible after the barrier below)
     for (int e = tid; e < ne; e += 64 * GB_WAVES) {
         int off = 0, all = 0;
-        for (int b = 0; b < nblk; ++b) {
-            const int c = ws[(size_t)b * ne + e];
-            off += b < (int)blockIdx.x ? c : 0;
-            all += c;
+        for (int b0 = 0; b0 < nblk; b0 += 8) {  // eight blocks' counts loaded at once (clamped: unconditional loads)
+            int c[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) c[q] = ws[(size_t)min(b0 + q, nblk - 1) * ne + e];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int b = b0 + q, v = b < nblk ? c[q] : 0;
+                off += b < (int)blockIdx.x ? v : 0;
+                all += v;
+            }
         }
         boff[e] = off;
         eoff[e] = all;
@@ -291,9 +314,7 @@ __global__ void __launch_bounds__(64 * GB_WAVES) k_group_place(const int* ids, i
         if (tid == 0) *n_tiles = nt;
     }
     int pk[NM], acc[NM];
-    if (tid == 0) lvmax = 0;
-    __syncthreads();
-    const int levels = group_levels(group_row<NM>(ids + (size_t)t * nu, nu, ne, t < T, pk), &lvmax);
+    const int levels = group_levels(group_row_keys<NM>(r, nu, ne, pk), &lvmax);
 #pragma unroll
     for (int j = 0; j < NM; ++j) acc[j] = 0;
     for (int k = 0; k < levels; ++k) {
