@@ -476,7 +476,7 @@ template <int TYPE, int NM, int KB>
 #define GG_WPE 3  // waves per SIMD asked of the compiler (0: its choice; 3 measured 3-8% faster than its 2)
 #endif
 #ifndef GG_WPE_D8
-#define GG_WPE_D8 5  // the same for the one-matrix Q8_0 kernel (96 VGPRs: five workgroups per CU)
+#define GG_WPE_D8 5  // the same for the one-matrix Q8_0 kernel (96 VGPRs: five workgroups per CU; 6 spilled, config 2 +13%)
 #endif
 __global__ void __launch_bounds__(256)
 #if GG_WPE
