@@ -35,6 +35,11 @@
 
 
 
+#ifndef FD_RANK_MAX_NE
+#define FD_RANK_MAX_NE 256  // the largest expert count routed by rank counting over the workgroup, else by one
+                            // wave (128, i.e. one wave at 256 experts: config 4 1,555 -> 1,447 tokens/s)
+#endif
+
 // ---- kernel 1: router logits (workgroups 0 .. NE - 1), x quantized (workgroup NE; Q4_K: E / 256 workgroups),
 // the shared gate (the last workgroup)
 __global__ void __launch_bounds__(256) k_fd_logits(FArgs a) {
@@ -649,7 +654,7 @@ bool moe_fused_try(const moe_layer_desc* d, const float* x, const float* logits,
     a.wts_out = wts_out;
     // Top-k by rank counting in kernel 2, the weights in an extra wave of kernel 3 (s_pk holds 256 keys; the
     // extra wave needs a 17th wave of room)
-    a.rank_route = a.NE <= 256 && a.NS < 16 ? 1 : 0;
+    a.rank_route = a.NE <= FD_RANK_MAX_NE && a.NS < 16 ? 1 : 0;
     *err = moe_fused_launch(d, a, scratch, kernels, st);
     return true;
 }
