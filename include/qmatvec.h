@@ -153,8 +153,12 @@ hipError_t qmatvec_pack_weights(int type, const void *W, size_t row_bytes, long 
 // The same with flags (0: as qmatvec_pack_weights):
 //   QMATVEC_PACK_INPLACE: the split planes replace the native rows in W itself (no copy: every launcher reads the
 //     planes, and a launch that would need W's native rows -- together with a matrix that is not registered --
-//     returns hipErrorInvalidValue). The call waits for the rewrite (it uses a transient buffer of the matrix's
-//     size); qmatvec_unpack_weights(W) writes the native rows back before it returns.
+//     returns hipErrorInvalidValue). The call waits for the rewrite, done in row chunks through a transient buffer of
+//     the matrix's scale bytes plus 16 MiB (never a full copy); qmatvec_unpack_weights(W) writes the native rows
+//     back the same way before it returns. If the transient buffer cannot be had, W is left untouched: the pack
+//     returns the error unregistered, the unpack returns it with the registration still in force. A failure after
+//     W has been partly rewritten leaves the matrix registered as unreadable (every launch that would touch it
+//     returns hipErrorInvalidValue) and returns the error; unregistering it then frees it without a restore.
 //   QMATVEC_PACK_NO_TILES: no operand tiles (prefill then runs the per-entry kernels on the planes).
 // Device memory held per matrix, W included: default 3x native for Q8_0 (3.56x FP4, 3.67x Q4_K); INPLACE 2x
 // (2.56x, 2.67x); INPLACE | NO_TILES 1x.
@@ -162,7 +166,11 @@ hipError_t qmatvec_pack_weights(int type, const void *W, size_t row_bytes, long 
 #define QMATVEC_PACK_NO_TILES 2
 hipError_t qmatvec_pack_weights_ex(int type, void *W, size_t row_bytes, long long rows, int K, int flags,
                                    hipStream_t stream);
-void qmatvec_unpack_weights(const void *W);
+// Unregisters W (see above); hipSuccess also for a W that is not registered.
+hipError_t qmatvec_unpack_weights(const void *W);
+// No counterpart in the reference (a test hook). The next fail_allocs transient buffers of in-place registration
+// and unregistration fail as out of memory; chunk_bytes sets the rewrite's row chunk (0: 16 MiB). Process-wide.
+void qmatvec_test_registry(int fail_allocs, long long chunk_bytes);
 // Device bytes the split-plane copy of such a matrix takes (the same as the native rows).
 size_t qmatvec_packed_bytes(int type, long long rows, int K);
 // Device bytes a registration with these flags allocates besides W (the copy and / or the tiles); 0 for a bad

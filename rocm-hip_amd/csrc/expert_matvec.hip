@@ -288,6 +288,8 @@ struct Packed {
     uint8_t* tiles;  // MFMA operand tiles (value tiles, then scale tiles), or nullptr
     bool inplace;    // the planes replaced the native rows in W
     uint8_t* alloc;  // the device memory the registration allocated (planes and / or tiles), or nullptr
+    bool broken;     // an in-place rewrite is under way or failed part-way: W holds neither layout whole, so no
+                     // launch may read it (find_* miss it, packed_in_place names it)
 };
 
 // Whether a registered matrix also gets MFMA operand tiles: a type of the MFMA kernels, whole 32-row groups and
@@ -319,7 +321,9 @@ bool find_packed(const void* W, int type, int K, size_t row_bytes, const uint8_t
     --it;
     const Packed& p = it->second;
     const uintptr_t off = (uintptr_t)W - it->first;
-    if ((uintptr_t)W >= p.end || p.type != type || p.K != K || p.row_bytes != row_bytes || off % row_bytes) return false;
+    if ((uintptr_t)W >= p.end || p.broken || p.type != type || p.K != K || p.row_bytes != row_bytes ||
+        off % row_bytes)
+        return false;
     const long long row = (long long)(off / row_bytes);
     *v = p.mem + row * fmt_value_row(type, K);
     *s = p.mem + (size_t)p.rows * fmt_value_row(type, K) + row * fmt_scale_row(type, K);
@@ -338,7 +342,7 @@ bool find_tiles(const void* W, int type, int K, size_t row_bytes, const uint8_t*
     --it;
     const Packed& p = it->second;
     const uintptr_t off = (uintptr_t)W - it->first;
-    if ((uintptr_t)W >= p.end || !p.tiles || p.type != type || p.K != K || p.row_bytes != row_bytes ||
+    if ((uintptr_t)W >= p.end || p.broken || !p.tiles || p.type != type || p.K != K || p.row_bytes != row_bytes ||
         off % (32 * row_bytes))
         return false;
     const long long g = (long long)(off / (32 * row_bytes));
@@ -493,50 +497,141 @@ static size_t packed_planes_bytes(int type, long long rows, int K) {
 }
 
 template <int TYPE>
-static hipError_t launch_pack(const void* W, size_t rb, long long rows, int K, uint8_t* mem, uint8_t* tiles,
+static hipError_t launch_tiles(const void* W, size_t rb, long long rows, int K, uint8_t* tiles, hipStream_t st) {
+    const long long nt = rows / 32 * (K / 32) * 64 + rows * (K / 256);
+    return launch_kernel(k_pack_tiles<TYPE>, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st, (const uint8_t*)W,
+                         (long long)rb, rows, K, tiles, tiles + (size_t)rows * tile_value_row(TYPE, K));
+}
+
+// Native rows W (rows of rb bytes) -> value rows at V and scale rows at S
+template <int TYPE>
+static hipError_t launch_pack(const void* W, size_t rb, long long rows, int K, uint8_t* V, uint8_t* S,
                               hipStream_t st) {
     constexpr int BV = TYPE == QT_Q4_K ? 256 : 32;
     const long long n = rows * (K / BV);
-    uint8_t* V = mem;
-    uint8_t* S = mem + (size_t)rows * fmt_value_row(TYPE, K);
-    hipError_t e = hipSuccess;
-    if (tiles) {  // the tiles first: an in-place registration overwrites W after them
-        const long long nt = rows / 32 * (K / 32) * 64 + rows * (K / 256);
-        e = launch_kernel(k_pack_tiles<TYPE>, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st,
-                          (const uint8_t*)W, (long long)rb, rows, K, tiles,
-                          tiles + (size_t)rows * tile_value_row(TYPE, K));  // scale tiles after the values
-    }
-    if (e == hipSuccess)
-        e = launch_kernel(k_pack<TYPE, false>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                          (const uint8_t*)W, (long long)rb, rows, K, V, S);
-    return e;
+    return launch_kernel(k_pack<TYPE, false>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const uint8_t*)W,
+                         (long long)rb, rows, K, V, S);
 }
 
+// Value rows V and scale rows S -> native rows W (unregistering a matrix packed in place)
 template <int TYPE>
-static hipError_t launch_unpack(uint8_t* W, size_t rb, long long rows, int K, uint8_t* planes, hipStream_t st) {
+static hipError_t launch_unpack(uint8_t* W, size_t rb, long long rows, int K, const uint8_t* V, const uint8_t* S,
+                                hipStream_t st) {
     constexpr int BV = TYPE == QT_Q4_K ? 256 : 32;
     const long long n = rows * (K / BV);
     return launch_kernel(k_pack<TYPE, true>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const uint8_t*)W,
-                         (long long)rb, rows, K, planes, planes + (size_t)rows * fmt_value_row(TYPE, K));
+                         (long long)rb, rows, K, (uint8_t*)V, (uint8_t*)S);
 }
 
-static hipError_t pack_type(int type, const void* W, size_t rb, long long rows, int K, uint8_t* planes, uint8_t* tiles,
+static hipError_t tiles_type(int type, const void* W, size_t rb, long long rows, int K, uint8_t* tiles,
+                             hipStream_t st) {
+#define CALL_(T) launch_tiles<T>(W, rb, rows, K, tiles, st)
+    switch (type) {
+    case QT_Q8_0: return CALL_(QT_Q8_0);
+    case QT_ROCMFP4: return CALL_(QT_ROCMFP4);
+    case QT_ROCMFP4_FAST: return CALL_(QT_ROCMFP4_FAST);
+    default: return CALL_(QT_Q4_K);
+    }
+#undef CALL_
+}
+
+static hipError_t pack_type(int type, const void* W, size_t rb, long long rows, int K, uint8_t* V, uint8_t* S,
                             hipStream_t st) {
+#define CALL_(T) launch_pack<T>(W, rb, rows, K, V, S, st)
     switch (type) {
-    case QT_Q8_0: return launch_pack<QT_Q8_0>(W, rb, rows, K, planes, tiles, st);
-    case QT_ROCMFP4: return launch_pack<QT_ROCMFP4>(W, rb, rows, K, planes, tiles, st);
-    case QT_ROCMFP4_FAST: return launch_pack<QT_ROCMFP4_FAST>(W, rb, rows, K, planes, tiles, st);
-    default: return launch_pack<QT_Q4_K>(W, rb, rows, K, planes, tiles, st);
+    case QT_Q8_0: return CALL_(QT_Q8_0);
+    case QT_ROCMFP4: return CALL_(QT_ROCMFP4);
+    case QT_ROCMFP4_FAST: return CALL_(QT_ROCMFP4_FAST);
+    default: return CALL_(QT_Q4_K);
     }
+#undef CALL_
 }
 
-static hipError_t unpack_type(int type, uint8_t* W, size_t rb, long long rows, int K, uint8_t* planes, hipStream_t st) {
+static hipError_t unpack_type(int type, uint8_t* W, size_t rb, long long rows, int K, const uint8_t* V,
+                              const uint8_t* S, hipStream_t st) {
+#define CALL_(T) launch_unpack<T>(W, rb, rows, K, V, S, st)
     switch (type) {
-    case QT_Q8_0: return launch_unpack<QT_Q8_0>(W, rb, rows, K, planes, st);
-    case QT_ROCMFP4: return launch_unpack<QT_ROCMFP4>(W, rb, rows, K, planes, st);
-    case QT_ROCMFP4_FAST: return launch_unpack<QT_ROCMFP4_FAST>(W, rb, rows, K, planes, st);
-    default: return launch_unpack<QT_Q4_K>(W, rb, rows, K, planes, st);
+    case QT_Q8_0: return CALL_(QT_Q8_0);
+    case QT_ROCMFP4: return CALL_(QT_ROCMFP4);
+    case QT_ROCMFP4_FAST: return CALL_(QT_ROCMFP4_FAST);
+    default: return CALL_(QT_Q4_K);
     }
+#undef CALL_
+}
+
+// ---- in-place rewrites through bounded staging: the whole scale plane (1/17 of a Q8_0 or FAST matrix, 1/9 of a
+// ROCmFP4 or Q4_K one) plus one chunk of rows, never a copy of the matrix
+//
+// Pack, rows ascending in chunks [a, b): the chunk's native rows are copied out, then its value rows written to
+// [a vrow, b vrow). Those bytes held native rows below b only (vrow < rb), all consumed by now or in the chunk;
+// the native rows at and past b (from b rb on) are untouched. The scale rows collect in the staging and land
+// after the value plane at the end, over native bytes every chunk has already consumed.
+// Unpack, the reverse, rows descending: the scale plane is copied out first; chunk [a, b)'s value rows are copied
+// out and its native rows written to [a rb, b rb), which holds only value rows at and past a (a vrow <= a rb) --
+// the chunk's own, already copied, and those of chunks done before it -- and the scale plane.
+
+static std::atomic<int> g_fail_allocs{0};         // test hook: fail this many of the next staging allocations
+static std::atomic<long long> g_chunk_bytes{16ll << 20};  // staging chunk (native bytes of whole rows)
+
+static hipError_t staging_alloc(void** p, size_t n) {
+    int f = g_fail_allocs.load();
+    while (f > 0)
+        if (g_fail_allocs.compare_exchange_weak(f, f - 1)) return hipErrorOutOfMemory;
+    return hipMalloc(p, n);
+}
+
+static long long chunk_rows(size_t rb, long long rows) {
+    const long long c = g_chunk_bytes.load() / (long long)rb;
+    return c < 1 ? 1 : c > rows ? rows : c;
+}
+
+// *started: whether W has been written (a failure after that leaves W in neither layout)
+static hipError_t pack_in_place(int type, uint8_t* W, size_t rb, long long rows, int K, hipStream_t st,
+                                bool* started) {
+    const size_t vrow = fmt_value_row(type, K), srow = fmt_scale_row(type, K);
+    const long long C = chunk_rows(rb, rows);
+    void* m = nullptr;
+    hipError_t e = staging_alloc(&m, (size_t)rows * srow + (size_t)C * rb);
+    if (e != hipSuccess) return e;
+    uint8_t* sst = (uint8_t*)m;
+    uint8_t* chunk = sst + (size_t)rows * srow;
+    for (long long a = 0; a < rows && e == hipSuccess; a += C) {
+        const long long n = rows - a < C ? rows - a : C;
+        e = hipMemcpyAsync(chunk, W + (size_t)a * rb, (size_t)n * rb, hipMemcpyDeviceToDevice, st);
+        *started = true;
+        if (e == hipSuccess) e = pack_type(type, chunk, rb, n, K, W + (size_t)a * vrow, sst + (size_t)a * srow, st);
+    }
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(W + (size_t)rows * vrow, sst, (size_t)rows * srow, hipMemcpyDeviceToDevice, st);
+    const hipError_t es = hipStreamSynchronize(st);  // the staging is freed next
+    (void)hipFree(m);
+    return e != hipSuccess ? e : es;
+}
+
+static hipError_t unpack_in_place(int type, uint8_t* W, size_t rb, long long rows, int K, bool* started) {
+    const size_t vrow = fmt_value_row(type, K), srow = fmt_scale_row(type, K);
+    const long long C = chunk_rows(rb, rows);
+    void* m = nullptr;
+    hipError_t e = staging_alloc(&m, (size_t)rows * srow + (size_t)C * vrow);
+    if (e != hipSuccess) return e;
+    uint8_t* sst = (uint8_t*)m;
+    uint8_t* chunk = sst + (size_t)rows * srow;
+    hipStream_t st = nullptr;  // the null stream, after a device synchronization
+    e = hipMemcpyAsync(sst, W + (size_t)rows * vrow, (size_t)rows * srow, hipMemcpyDeviceToDevice, st);
+    for (long long b = rows; b > 0 && e == hipSuccess; b -= C) {
+        const long long a = b > C ? b - C : 0, n = b - a;
+        e = hipMemcpyAsync(chunk, W + (size_t)a * vrow, (size_t)n * vrow, hipMemcpyDeviceToDevice, st);
+        *started = true;
+        if (e == hipSuccess) e = unpack_type(type, W + (size_t)a * rb, rb, n, K, chunk, sst + (size_t)a * srow, st);
+    }
+    const hipError_t es = hipStreamSynchronize(st);
+    (void)hipFree(m);
+    return e != hipSuccess ? e : es;
+}
+
+extern "C" void qmatvec_test_registry(int fail_allocs, long long chunk_bytes) {
+    g_fail_allocs.store(fail_allocs > 0 ? fail_allocs : 0);
+    g_chunk_bytes.store(chunk_bytes > 0 ? chunk_bytes : 16ll << 20);
 }
 
 static size_t tile_bytes_of(int type, long long rows, int K, int flags) {
@@ -575,32 +670,27 @@ extern "C" hipError_t qmatvec_pack_weights_ex(int type, void* W, size_t row_byte
     }
     uint8_t* tiles = tile_bytes ? alloc + (inplace ? 0 : planes) : nullptr;
     hipError_t e = hipSuccess;
-    if (!inplace) {
-        e = pack_type(type, W, row_bytes, rows, K, alloc, tiles, stream);
-    } else {
-        // the planes go to a transient buffer (a block's native bytes and its plane bytes overlap other blocks'),
-        // then over W; the call waits for the copy so that the transient buffer can be freed
-        void* tmp = nullptr;
-        e = hipMalloc(&tmp, planes);
-        if (e == hipSuccess) {
-            e = pack_type(type, W, row_bytes, rows, K, (uint8_t*)tmp, tiles, stream);
-            if (e == hipSuccess) e = hipMemcpyAsync(W, tmp, planes, hipMemcpyDeviceToDevice, stream);
-            const hipError_t es = hipStreamSynchronize(stream);
-            if (e == hipSuccess) e = es;
-            (void)hipFree(tmp);
-        }
+    if (tiles) e = tiles_type(type, W, row_bytes, rows, K, tiles, stream);  // from the native rows, first
+    bool started = false;  // (in place) whether W has been written
+    if (e == hipSuccess) {
+        if (!inplace)
+            e = pack_type(type, W, row_bytes, rows, K, alloc, alloc + (size_t)rows * fmt_value_row(type, K), stream);
+        else
+            e = pack_in_place(type, (uint8_t*)W, row_bytes, rows, K, stream, &started);
     }
-    if (e != hipSuccess) {
+    if (e != hipSuccess && !started) {
         if (alloc) {
             (void)hipStreamSynchronize(stream);
             (void)hipFree(alloc);
         }
         return e;
     }
+    // registered on success; after a failure part-way through an in-place rewrite, registered as broken, so that
+    // no launch reads W as either layout (unregistering then drops it without a restore)
     std::lock_guard<std::mutex> lk(g_pack_mu);
     g_packed[(uintptr_t)W] = Packed{(uintptr_t)W + bytes, type, K, row_bytes, rows,
-                                    inplace ? (uint8_t*)W : alloc, tiles, inplace, alloc};
-    return hipSuccess;
+                                    inplace ? (uint8_t*)W : alloc, tiles, inplace, alloc, e != hipSuccess};
+    return e;
 }
 
 extern "C" hipError_t qmatvec_pack_weights(int type, const void* W, size_t row_bytes, long long rows, int K,
@@ -608,28 +698,34 @@ extern "C" hipError_t qmatvec_pack_weights(int type, const void* W, size_t row_b
     return qmatvec_pack_weights_ex(type, (void*)W, row_bytes, rows, K, 0, stream);
 }
 
-extern "C" void qmatvec_unpack_weights(const void* W) {
+extern "C" hipError_t qmatvec_unpack_weights(const void* W) {
     Packed p;
     {
         std::lock_guard<std::mutex> lk(g_pack_mu);
         auto it = g_packed.find((uintptr_t)W);
-        if (it == g_packed.end()) return;
+        if (it == g_packed.end()) return hipSuccess;
         p = it->second;
-        g_packed.erase(it);
-    }
-    // launches already queued on any stream may still read the copy (or, packed in place, W's planes)
-    if (hipDeviceSynchronize() != hipSuccess) return;
-    if (p.inplace) {  // the native rows back into W, through a transient copy of the planes
-        const size_t planes = packed_planes_bytes(p.type, p.rows, p.K);
-        void* tmp = nullptr;
-        if (hipMalloc(&tmp, planes) == hipSuccess) {
-            if (hipMemcpy(tmp, W, planes, hipMemcpyDeviceToDevice) == hipSuccess &&
-                unpack_type(p.type, (uint8_t*)W, p.row_bytes, p.rows, p.K, (uint8_t*)tmp, nullptr) == hipSuccess)
-                (void)hipDeviceSynchronize();
-            (void)hipFree(tmp);
+        if (!p.inplace || p.broken) {
+            g_packed.erase(it);
+        } else {
+            it->second.broken = true;  // no new launch reads it while the native rows come back
         }
     }
+    // launches already queued on any stream may still read the copy (or, packed in place, W's planes)
+    hipError_t e = hipDeviceSynchronize();
+    if (p.inplace && !p.broken) {
+        bool started = false;
+        if (e == hipSuccess) e = unpack_in_place(p.type, (uint8_t*)W, p.row_bytes, p.rows, p.K, &started);
+        std::lock_guard<std::mutex> lk(g_pack_mu);
+        auto it = g_packed.find((uintptr_t)W);
+        if (e != hipSuccess) {  // still registered: usable again if W was not touched, else broken
+            if (it != g_packed.end()) it->second.broken = started;
+            return e;
+        }
+        if (it != g_packed.end()) g_packed.erase(it);
+    }
     if (p.alloc) (void)hipFree(p.alloc);
+    return e;
 }
 
 // The per-operation kernels' lane shape for a row of K values (the fused layer kernel copies it)
@@ -650,7 +746,8 @@ bool moe_packed_tiles(const void* W, int type, int K, size_t row_bytes, const ui
     return find_tiles(W, type, K, row_bytes, vt, st, vgs, sgs);
 }
 
-// Drop every registration (library teardown)
+// Drop every registration (library teardown). Matrices packed in place keep their planes: W may already be gone
+// here, so teardown writes nothing into it
 void moe_unpack_all(void) {
     std::map<uintptr_t, Packed> all;
     {

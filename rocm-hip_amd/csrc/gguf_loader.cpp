@@ -723,7 +723,7 @@ void moe_gguf_layer_release(moe_gguf_layer* l) {
         const void* w[6] = {l->desc.w_gate, l->desc.w_up, l->desc.w_down, l->desc.s_gate, l->desc.s_up,
                             l->desc.s_down};
         for (const void* p : w)
-            if (p) qmatvec_unpack_weights(p);
+            if (p) (void)qmatvec_unpack_weights(p);  // (the device copy is freed next either way)
     }
     if (l->dev) (void)hipFree(l->dev);
     memset(l, 0, sizeof(*l));

@@ -22,6 +22,7 @@ int moe_device_cus(void) { return g_cus.load(std::memory_order_relaxed); }
 extern "C" int moe_lib_ready(void) { return g_ready.load(std::memory_order_acquire); }
 
 void moe_unpack_all(void);
+void moe_noalloc_forget(void);
 
 static int init_device(void) {
     if (g_ready.load()) return 0;
@@ -40,7 +41,10 @@ extern "C" int qmatvec_init(const char* co_path) {
     return init_device();
 }
 
-extern "C" void qmatvec_free(void) { moe_unpack_all(); }
+extern "C" void qmatvec_free(void) {
+    moe_unpack_all();
+    moe_noalloc_forget();
+}
 
 extern "C" int gpu_ops_init(const char* co_path) {
     (void)co_path;

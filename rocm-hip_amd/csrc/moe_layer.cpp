@@ -238,27 +238,33 @@ static hipError_t layer_forward(const moe_layer_desc* d, const float* x, const f
                 shared_done = true;
             }
         } else {
-            CHECK(qmatvec_launch_q8_id_batch(type, d->w_gate, rb_in, &qx, g, FE, E, p.max_tiles, p.tile, ntile, te,
-                                             ts, tn, tok, pair, st));
-            CHECK(qmatvec_launch_q8_id_batch(type, d->w_up, rb_in, &qx, u, FE, E, p.max_tiles, p.tile, ntile, te, ts,
-                                             tn, tok, pair, st));
-            CHECK(moe_swiglu_q8(g, u, nullptr, T * NU * FE, &qa, st, type == 12 ? 2 : 1));
-            CHECK(qmatvec_launch_q8_id_batch(type, d->w_down, rb_out, &qa, down, E, FE, p.max_tiles, p.tile, ntile, te,
-                                             ts, tn, pair, pair, st));
+            if (pm & 2) {
+                CHECK(qmatvec_launch_q8_id_batch(type, d->w_gate, rb_in, &qx, g, FE, E, p.max_tiles, p.tile, ntile,
+                                                 te, ts, tn, tok, pair, st));
+                CHECK(qmatvec_launch_q8_id_batch(type, d->w_up, rb_in, &qx, u, FE, E, p.max_tiles, p.tile, ntile, te,
+                                                 ts, tn, tok, pair, st));
+                CHECK(moe_swiglu_q8(g, u, nullptr, T * NU * FE, &qa, st, type == 12 ? 2 : 1));
+            }
+            if (pm & 4)
+                CHECK(qmatvec_launch_q8_id_batch(type, d->w_down, rb_out, &qa, down, E, FE, p.max_tiles, p.tile,
+                                                 ntile, te, ts, tn, pair, pair, st));
         }
-        if (!sh) CHECK(gpu_moe_combine(down, wts, nullptr, nullptr, out, NU, E, T, st));
+        if (!sh && (pm & 8)) CHECK(gpu_moe_combine(down, wts, nullptr, nullptr, out, NU, E, T, st));
     }
     if (sh && !slot && !shared_done) {  // the shared expert as a dense FFN on all T tokens, then the combine
         float* sgt = (float*)(s + p.sg_);
         float* sut = (float*)(s + p.su);
         float* sout = (float*)(s + p.sout);
         qmatvec_q8_bind(&qs, s + p.qs, p.qs_k);
-        CHECK(qmatvec_launch_q8_batch(type, d->s_gate, rb_in, &qx, sgt, FE, FE, E, T, st));
-        CHECK(qmatvec_launch_q8_batch(type, d->s_up, rb_in, &qx, sut, FE, FE, E, T, st));
-        CHECK(moe_swiglu_q8(sgt, sut, nullptr, T * FE, &qs, st, type == 12 ? 2 : 1));
-        CHECK(qmatvec_launch_q8_batch(type, d->s_down, rb_out, &qs, sout, E, E, FE, T, st));
-        CHECK(gpu_moe_combine(down, wts, sout, d->w_shexp ? sg : nullptr, out, NU, E, T, st));
+        if (pm & 2) {  // (the prefill profiling subsets: its gate / up with the routed ones', its down with down)
+            CHECK(qmatvec_launch_q8_batch(type, d->s_gate, rb_in, &qx, sgt, FE, FE, E, T, st));
+            CHECK(qmatvec_launch_q8_batch(type, d->s_up, rb_in, &qx, sut, FE, FE, E, T, st));
+            CHECK(moe_swiglu_q8(sgt, sut, nullptr, T * FE, &qs, st, type == 12 ? 2 : 1));
+        }
+        if (pm & 4) CHECK(qmatvec_launch_q8_batch(type, d->s_down, rb_out, &qs, sout, E, E, FE, T, st));
+        if (pm & 8) CHECK(gpu_moe_combine(down, wts, sout, d->w_shexp ? sg : nullptr, out, NU, E, T, st));
     }
+    if (!(pm & 8)) return hipSuccess;  // (a profiling subset: the results are not complete)
     const int ns_used = slot ? NU + 1 : NU;
     if (ids_out)
         CHECK(hipMemcpy2DAsync(ids_out, (size_t)NU * 4, ids, (size_t)ns_used * 4, (size_t)NU * 4, T,
@@ -294,9 +300,11 @@ extern "C" hipError_t moe_layer_forward_norm(const moe_layer_desc* d, const floa
     if (T >= 8) {  // the prefill: the norm writes y's quantized bundle too, where its wave path applies
         qmatvec_q8 qx;
         qmatvec_q8_bind(&qx, (char*)scratch + p.qx, p.qx_k);
-        if (moe_add_rmsnorm_q8(x_in, add, x_out, w_norm, y, d->n_embd, T, eps, &qx, d->type == 12 ? 2 : 1, st) ==
-            hipSuccess)
+        const hipError_t e =
+            moe_add_rmsnorm_q8(x_in, add, x_out, w_norm, y, d->n_embd, T, eps, &qx, d->type == 12 ? 2 : 1, st);
+        if (e == hipSuccess)
             return layer_forward(d, y, logits, T, out, ids_out, wts_out, scratch, scratch_bytes, st, true);
+        if (e != hipErrorInvalidValue) return e;  // (invalid value: its wave path does not take this row length)
     }
     CHECK(gpu_add_rmsnorm(x_in, add, x_out, w_norm, y, d->n_embd, T, eps, nullptr, st));
     return layer_forward(d, y, logits, T, out, ids_out, wts_out, scratch, scratch_bytes, st, false);

@@ -6,7 +6,9 @@
 // name to a kernel (on the host it is a stand-in, not a device address): the first call on a device, with that
 // device current, looks up the device address with hipGetSymbolAddress and keeps it per device. Every call on a
 // device shares that device's array, so calls that overlap on one GPU (two streams, two threads) race; the layer
-// writes every scratch byte it reads, so nothing needs clearing between calls.
+// writes every scratch byte it reads, so nothing needs clearing between calls. qmatvec_free drops the looked-up
+// addresses (moe_noalloc_forget), so that a later call after a device reset or a reload of the code object looks
+// them up again.
 
 #include <hip/hip_runtime.h>
 
@@ -37,6 +39,12 @@ static hipError_t scratch_ptr(void** out) {
     }
     *out = g_ptr[dev];
     return hipSuccess;
+}
+
+// Forget every looked-up address (library teardown)
+void moe_noalloc_forget(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (void*& p : g_ptr) p = nullptr;
 }
 
 extern "C" hipError_t moe_layer_forward_noalloc(const moe_layer_desc* d, const float* x, const float* logits, int T,

@@ -75,6 +75,8 @@ hipError_t core_one(moe_engine& e, const moe_engine_layer& L, float* out, hipStr
     TRY(gpu_swiglu(e.g, e.u, e.act, NS * FE, &e.q8, st));
     TRY(qmatvec_launch_q8_id_x(L.exp_down.type, L.exp_down.data, nullptr, L.sh_down.data, nullptr,
                                L.exp_down.row_bytes, e.ids, NS, 1, &e.q8, e.down, nullptr, E, FE, 1, st));
+    // (qwen_model.cpp:933 passes s.sg whether or not there is a gate vector; with none its router leaves sg
+    // unwritten, so NULL here -- a weight of 1 for the shared row -- is the same result without reading it)
     return gpu_moe_combine(e.down, e.wts, e.down + (size_t)NU * E, L.shexp_gate ? e.sg : nullptr, out, NU, E, 1, st);
 }
 
@@ -124,6 +126,7 @@ hipError_t core(moe_engine& e, const moe_engine_layer& L, int T, float* out, hip
     if (!L.sh_gate.data) return gpu_moe_combine(e.down, e.wts, nullptr, nullptr, out, NU, E, T, st);
     TRY(gpu_swiglu(e.sg_g, e.sg_u, e.sact, T * FS, &e.q8, st));
     TRY(matvec_q8(L.sh_down, &e.q8, e.sout, T, st));
+    // (NULL without a gate vector, as above)
     return gpu_moe_combine(e.down, e.wts, e.sout, L.shexp_gate ? e.sg : nullptr, out, NU, E, T, st);
 }
 

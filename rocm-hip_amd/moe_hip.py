@@ -62,7 +62,8 @@ SIGNATURES = {
     "qmatvec_q8_id_batch_supported": (_I, [_I, _I]),
     "qmatvec_launch_q8_id_batch": (_I, [_I, _P, _Z, _Q8P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "qmatvec_pack_weights": (_I, [_I, _P, _Z, _L, _I, _P]),
-    "qmatvec_unpack_weights": (None, [_P]),
+    "qmatvec_unpack_weights": (_I, [_P]),
+    "qmatvec_test_registry": (None, [_I, _L]),
     "qmatvec_pack_weights_ex": (_I, [_I, _P, _Z, _L, _I, _I, _P]),
     "qmatvec_registered_bytes": (_Z, [_I, _L, _I, _I]),
     "qmatvec_packed_bytes": (_Z, [_I, _L, _I]),

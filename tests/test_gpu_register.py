@@ -128,3 +128,52 @@ def test_inplace_matrix_is_not_read_as_native_rows(moe, oracle):
         torch.cuda.synchronize()
         moe.qmatvec_unpack_weights(cvoid(d["w_gate"]))
         moe.qmatvec_unpack_weights(cvoid(d["s_gate"]))
+
+
+OUT_OF_MEMORY = 2
+
+
+@pytest.mark.parametrize("qtype,flags", [(Q8_0, INPLACE), (FP4, INPLACE | NO_TILES), (Q4_K, INPLACE), (FAST, INPLACE)])
+def test_inplace_rewrite_failures_and_chunks(moe, oracle, qtype, flags):
+    """In-place registration runs in row chunks through a bounded transient buffer (here 3 rows' worth, so every
+    chunk boundary case occurs) and restores W bit for bit. When the transient buffer cannot be had, pack leaves
+    W untouched and unregistered, and unpack leaves the registration in force and usable."""
+    announce("inplace chunks / failures", qtype, flags)
+    spec = synth.LayerSpec(qtype, 512, 8, 2, 256, False)
+    L = synth.make_layer(spec, seed=97 + qtype)
+    rows, K = spec.NE * spec.FE, spec.E
+    rb = moe_hip.row_size(qtype, K)
+    d = {k: dev(v) for k, v in L.items()}
+    W = d["w_gate"]
+    q = moe_hip.Q8Buffer(moe, K)
+    x = np.random.default_rng(98).standard_normal(K).astype(np.float32)
+    moe.qmatvec_quantize(cvoid(dev(x)), K, q.ref(), S())
+    ids = dev(np.array([5, 1], np.int32))
+    want = np.stack([oracle.matvec(qtype, L["w_gate"][e * spec.FE:(e + 1) * spec.FE], x, spec.FE, K) for e in (5, 1)])
+
+    def run():
+        y = zeros((2, spec.FE), torch.float32)
+        e = moe.lib.qmatvec_launch_q8_id(qtype, cvoid(W), rb, cvoid(ids), 2, 0, q.ref(), cvoid(y), spec.FE, K, 1, S())
+        return e, (host(y) if e == 0 else None)
+    try:
+        moe.lib.qmatvec_test_registry(1, 3 * rb)  # the pack's transient buffer fails
+        assert moe.lib.qmatvec_pack_weights_ex(qtype, cvoid(W), rb, rows, K, flags, S()) == OUT_OF_MEMORY
+        assert np.array_equal(host(W), L["w_gate"])  # untouched, and read as native rows
+        e, y = run()
+        assert e == 0 and rel_l2(y, want) < 1e-5
+        assert moe.lib.qmatvec_pack_weights_ex(qtype, cvoid(W), rb, rows, K, flags, S()) == 0
+        assert not np.array_equal(host(W), L["w_gate"])
+        e, y_packed = run()
+        assert e == 0 and rel_l2(y_packed, want) < 1e-5
+        moe.lib.qmatvec_test_registry(1, 3 * rb)  # the unpack's transient buffer fails: still registered
+        assert moe.lib.qmatvec_unpack_weights(cvoid(W)) == OUT_OF_MEMORY
+        e, y = run()
+        assert e == 0 and np.array_equal(y, y_packed)
+        assert moe.lib.qmatvec_unpack_weights(cvoid(W)) == 0
+        assert np.array_equal(host(W), L["w_gate"])  # the native rows back, bit for bit
+        e, y = run()
+        assert e == 0 and rel_l2(y, want) < 1e-5
+    finally:
+        moe.lib.qmatvec_test_registry(0, 0)
+        torch.cuda.synchronize()
+        moe.lib.qmatvec_unpack_weights(cvoid(W))
