@@ -193,7 +193,8 @@ __device__ __forceinline__ void load_x(const int8_t* q, const float* d, const in
 }
 
 // ---- one unit's float term: the integer block dots, then the reference's float combination
-// Q8_0: (d_w dx) * sum (src/matvec_q.hip:1530-1536); ROCmFP4: e0 dx s0 + e1 dx s1 (:1287-1289);
+// Q8_0: (d_w dx) * sum (src/matvec_q.hip:1530-1536); ROCmFP4: e0 dx s0 + e1 dx s1 (:1287-1289; e dx formed as
+// (2 e)(dx / 2), the same bits);
 // FAST: e dx (s0 + s1) (:1456-1466); Q4_K: d dx (sc0 slo + sc1 shi) - dmin dx (m0 (bs0 + bs1) + m1 (bs2 + bs3))
 // (:1740-1746, summed per 64-value chunk).
 template <int TYPE>
@@ -214,8 +215,9 @@ __device__ __forceinline__ float unit_term<QT_ROCMFP4>(const WUnit<QT_ROCMFP4>& 
         s0 = dot4((int)fp4x4_to_i8x4(w.q[k]), x.x[k], s0);
         s1 = dot4((int)fp4x4_to_i8x4(w.q[k] >> 4), x.x[4 + k], s1);
     }
-    const float e0 = ue4m3_half(w.s[0] & 0xffu), e1 = ue4m3_half((w.s[0] >> 8) & 0xffu);
-    return e0 * x.d * (float)s0 + e1 * x.d * (float)s1;
+    // e0 dx as (2 e0)(dx / 2): the same bits (both factors exact), the scale byte decoded by the converter
+    const float dxh = 0.5f * x.d, e0 = ue4m3_x2<0>(w.s[0]), e1 = ue4m3_x2<1>(w.s[0]);
+    return e0 * dxh * (float)s0 + e1 * dxh * (float)s1;
 }
 template <>
 __device__ __forceinline__ float unit_term<QT_ROCMFP4_FAST>(const WUnit<QT_ROCMFP4_FAST>& w,
@@ -226,7 +228,7 @@ __device__ __forceinline__ float unit_term<QT_ROCMFP4_FAST>(const WUnit<QT_ROCMF
         s0 = dot4((int)fp4x4_to_i8x4(w.q[k]), x.x[k], s0);
         s1 = dot4((int)fp4x4_to_i8x4(w.q[k] >> 4), x.x[4 + k], s1);
     }
-    return ue4m3_half(w.s[0] & 0xffu) * x.d * (float)(s0 + s1);
+    return ue4m3_x2<0>(w.s[0]) * (0.5f * x.d) * (float)(s0 + s1);
 }
 // Q4_K needs the chunk index c = u & 3 for its sub-block scales
 __device__ __forceinline__ float unit_term_q4k(const WUnit<QT_Q4_K>& w, const XUnit<QT_Q4_K>& x, int c) {

@@ -96,15 +96,32 @@ __device__ __forceinline__ float ue4m3_half(uint32_t e) {
 // Signed int8 dot of four bytes, accumulated (v_dot4_i32_i8)
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
-// Four FP4 codes (the low nibble of each byte) -> four int8 codebook values {0,1,2,3,4,6,8,10} with bit 3 the
-// sign. v_perm_b32 picks byte (code & 7) of an 8-byte table of magnitudes and of one of negatives; a third
-// v_perm_b32 takes byte k of the magnitudes (selector k) or of the negatives (k + 4, bit 3 moved to bit 2).
-// (All full-rate: a byte mask made by multiplying the sign bits by 0xff was a quarter-rate v_mul_lo_u32.)
+// Four FP4 codes (the low nibble of each byte) -> four int8 codebook values (Codebook10: nibbles 0..7 ->
+// +{0, 1, 2, 3, 4, 6, 8, 10}, 8..15 their negatives; src/fp4_common.h:29-33) as the XOR of two v_perm_b32 table
+// lookups. v_perm_b32 maps a selector byte c < 8 to byte c of its 8-byte table, 8..11 to 0x00 / 0xFF by the sign
+// bit of table byte 1 / 3 / 5 / 7, 12 to 0x00 and 13..15 to 0xFF. A = perm(TA, c) and B = perm(TB, c ^ 8) thus give
+// table bytes for c < 8 (A) and c >= 8 (B) and a 0x00 / 0xFF byte from the other table's signs; FP4_TA / FP4_TB are
+// the one pair of tables (an exhaustive search over the eight sign bits those selectors read) with A ^ B the
+// codebook value for all 16 codes. Five operations per four codes, where a magnitude and a negative lookup and a
+// third, sign-selecting v_perm_b32 took seven.
+#define FP4_TA_HI 0xf5f7f904u  // table bytes 4..7
+#define FP4_TA_LO 0x030201ffu  // table bytes 0..3
+#define FP4_TB_HI 0x090705fcu
+#define FP4_TB_LO 0x0201ff00u
 __device__ __forceinline__ uint32_t fp4x4_to_i8x4(uint32_t n) {
-    const uint32_t sel = n & 0x07070707u;
-    const uint32_t pos = __builtin_amdgcn_perm(0x0a080604u, 0x03020100u, sel);
-    const uint32_t neg = __builtin_amdgcn_perm(0xf6f8fafcu, 0xfdfeff00u, sel);
-    return __builtin_amdgcn_perm(neg, pos, ((n >> 1) & 0x04040404u) | 0x03020100u);
+    const uint32_t c = n & 0x0f0f0f0fu;
+    return __builtin_amdgcn_perm(FP4_TA_HI, FP4_TA_LO, c) ^ __builtin_amdgcn_perm(FP4_TB_HI, FP4_TB_LO, c ^ 0x08080808u);
+}
+
+// Twice the UE4M3 half-scale value of byte SEL of s (ue4m3_half's value times 2): the byte read as an OCP FP8 E4M3
+// value by gfx950's converter (exact for every byte; (8 + m) 2^(e - 10) normal, m 2^-9 subnormal, as the half
+// scale's (8 + m) 2^(e - 11) and m 2^-10 doubled), and 0 for the bytes 0x7f and above, which the converter reads
+// as NaN or negative. The kernels fold the 1/2 into the activation scale, an exact factor, so that e dx is formed
+// bit for bit as before. Three operations where the bit assembly took about eight.
+template <int SEL>
+__device__ __forceinline__ float ue4m3_x2(uint32_t s) {
+    const float c = __builtin_amdgcn_cvt_f32_fp8((int)s, SEL);
+    return c > 0.0f ? c : 0.0f;
 }
 
 // Q4_K 6-bit scale / min of sub-block j from the 12 scale bytes held as three dwords s[0..2]

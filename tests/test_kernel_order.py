@@ -135,3 +135,59 @@ def test_decode_departure_explained(oracle, case, tok, gpu_err, part):
                          None if sgt is None else np.float32(sgt))
     assert _rel(out_o, want[tok]) < 1e-7
     assert abs(_rel(ref, want[tok]) - gpu_err) <= 0.01 * gpu_err
+
+
+# ---------------------------------------------------------------- the decode kernels' FP4 and scale-byte decoding
+
+def _perm_byte(table8, sel):
+    """v_perm_b32's byte select (gfx9 ISA): table8 = bytes 0..7 of {src0, src1} (src1 the low four)."""
+    if sel >= 13:
+        return 0xff
+    if sel == 12:
+        return 0
+    if sel >= 8:
+        return 0xff if table8[2 * (sel - 8) + 1] & 0x80 else 0
+    return table8[sel]
+
+
+def _header_constant(name):
+    import re
+    path = __import__("os").path.join(__import__("os").path.dirname(__file__), "..", "rocm-hip_amd", "csrc",
+                                      "moe_common.h")
+    m = re.search(r"#define %s (0x[0-9a-f]+)u" % name, open(path).read())
+    return int(m.group(1), 16)
+
+
+def test_fp4_decode_tables_give_codebook10():
+    """fp4x4_to_i8x4 (moe_common.h): perm(TA, c) ^ perm(TB, c ^ 8) equals Codebook10 (the reference's
+    src/fp4_common.h:29-33: nibbles 0..7 +{0,1,2,3,4,6,8,10}, 8..15 negative) for every code, the tables read from
+    the header the kernels compile."""
+    def bytes8(hi, lo):
+        return [(lo >> (8 * i)) & 0xff for i in range(4)] + [(hi >> (8 * i)) & 0xff for i in range(4)]
+    ta = bytes8(_header_constant("FP4_TA_HI"), _header_constant("FP4_TA_LO"))
+    tb = bytes8(_header_constant("FP4_TB_HI"), _header_constant("FP4_TB_LO"))
+    cb = [0, 1, 2, 3, 4, 6, 8, 10, 0, -1, -2, -3, -4, -6, -8, -10]
+    for c in range(16):
+        got = _perm_byte(ta, c) ^ _perm_byte(tb, c ^ 8)
+        assert np.int8(np.uint8(got)) == cb[c], c
+
+
+def _e4m3(b):
+    """OCP FP8 E4M3 (the gfx950 converter's format) of byte b: sign, 4 exponent bits (bias 7), 3 mantissa bits;
+    0x7f / 0xff NaN."""
+    s, e, m = b >> 7, (b >> 3) & 15, b & 7
+    if e == 15 and m == 7:
+        return float("nan")
+    v = (m / 8.0) * 2.0 ** -6 if e == 0 else (1 + m / 8.0) * 2.0 ** (e - 7)
+    return -v if s else v
+
+
+def test_scale_byte_decode_equals_half_scale_doubled():
+    """ue4m3_x2 (moe_common.h): the E4M3 value of the byte, with NaN and negative readings (bytes 0x7f and up) made
+    0, is twice the UE4M3 half-scale value (synth.ue4m3_half_table, the reference's src/quant_types.cpp:352-357
+    restated) for all 256 bytes."""
+    half = synth.ue4m3_half_table()
+    for b in range(256):
+        c = _e4m3(b)
+        c = c if c > 0 else 0.0  # (NaN compares false)
+        assert np.float32(c) == np.float32(2.0) * half[b], b
