@@ -68,29 +68,37 @@ __global__ void __launch_bounds__(256) k_fm_logits(FArgs a) {
     stamp(a, 1);
 }
 
-// The union of the routed experts (set bits of an NE-bit map, ascending) and the shared expert (-1) after them:
-// slot u's expert, or -2 past the end. One thread.
-__device__ __forceinline__ int union_expert(const uint32_t* bits, int ne, int u, bool shared) {
-    int count = 0;
-    for (int wd = 0; wd < (ne + 31) / 32; ++wd) {
-        const uint32_t m = bits[wd];
-        const int c = __popc(m);
-        if (u < count + c) {
-            uint32_t mm = m;
-            for (int k = 0; k < u - count; ++k) mm &= mm - 1;  // drop the lower set bits
-            return 32 * wd + __ffs(mm) - 1;
-        }
-        count += c;
-    }
-    return shared && u == count ? -1 : -2;
-}
-
 // Token t's slot holding expert e (e = -1: the shared slot NU), -1 if t did not choose e
 __device__ __forceinline__ int slot_of(const int* ids_t, int nu, int e) {
     if (e == -1) return nu;
     for (int j = 0; j < nu; ++j)
         if (ids_t[j] == e) return j;
     return -1;
+}
+
+// The union of the T tokens' chosen experts (ids[t][0..nu), row stride 64), ascending, then the shared expert (-1)
+// when there is one: ulist[0..n), *count = n. One wave, in LDS byte flags (flag[ne], 4-byte aligned): the flags
+// cleared, every id's flag set (lanes 0 .. T nu - 1, one id each; a wave's LDS operations complete in order), then
+// lane l reads the flags of experts l, l + 64, ... and a ballot gives each chosen expert its place among the
+// chosen below it. (LDS atomics from T nu threads onto a bit map and one thread walking it took ~1.3 µs at T = 4;
+// a loop testing every id lane by lane, ~1.5 µs of dependent scalar steps.)
+__device__ __forceinline__ void form_union(const int (*ids)[64], int T, int nu, int ne, bool shared, uint8_t* flag,
+                                           int* ulist, int* count) {
+    const int lane = threadIdx.x & 63, tn = T * nu;
+    for (int i = lane; i < (ne + 3) / 4; i += 64) ((uint32_t*)flag)[i] = 0u;
+    if (lane < tn) flag[ids[lane / nu][lane % nu]] = 1;
+    int n = 0;
+    for (int e0 = 0; e0 < ne; e0 += 64) {  // (uniform)
+        const int e = e0 + lane;
+        const bool hit = e < ne && flag[e] != 0;
+        const uint64_t m = __ballot(hit);
+        if (hit) ulist[n + __popcll(m & ((1ull << lane) - 1))] = e;
+        n += __popcll(m);
+    }
+    if (lane == 0) {
+        if (shared) ulist[n] = -1;
+        *count = n + (shared ? 1 : 0);
+    }
 }
 
 // ---- kernel 2 (persistent: a workgroup per CU): routing of every token and the union, once per workgroup; then
@@ -109,8 +117,8 @@ __global__ void __launch_bounds__(1024) k_fm_gate_up(FArgs a) {
     constexpr bool Q8K = Fmt<TYPE>::Q8K;
     __shared__ int s_ids[FD_MAX_T][64];
     __shared__ float s_wts[FD_MAX_T][64];
-    __shared__ uint32_t bits[ROUTER_MAX_E / 32];
     __shared__ int ulist[FM_MAX_U], s_nu;
+    __shared__ __align__(4) uint8_t s_flag[ROUTER_MAX_E];
     __shared__ int s_slot[2][FD_MAX_T];
     __shared__ float gu[2][2][FD_MAX_T][32];  // [half][gate / up][token][row]
     // every token's quantized x, staged once: Q8_0 values [T][E] and scales [T][E / 32], or Q8_K values, scales
@@ -122,7 +130,6 @@ __global__ void __launch_bounds__(1024) k_fm_gate_up(FArgs a) {
     const int h = w / WPU, hw = w - h * WPU;  // unit of the round, wave within it
     const int T = a.T, FE = a.FE, NU = a.NU, NE = a.NE, nbf = FE / 32, nu_in = fmt_units(TYPE, a.E);
     stamp(a, 2);
-    for (int i = tid; i < (NE + 31) / 32; i += 1024) bits[i] = 0u;
     const float* lg = a.logits_in ? a.logits_in : a.logits;
     if (w < T) {
         router_select_one_wave(lg + (size_t)w * NE, NE, NU, s_ids[w], s_wts[w]);
@@ -136,25 +143,14 @@ __global__ void __launch_bounds__(1024) k_fm_gate_up(FArgs a) {
             for (int i = i0; i < TE / 64; i += n) ((int4*)s_xbs)[i] = ((const int4*)a.xo.bsK)[i];
     }
     __syncthreads();
-    if (tid < T * NU) {
+    if (blockIdx.x == 0 && tid < T * NU) {  // the routing for kernel 3 and the caller
         const int t = tid / NU, j = tid - t * NU;
-        const int e = s_ids[t][j];
-        atomicOr(&bits[e >> 5], 1u << (e & 31));
-        if (blockIdx.x == 0) {  // the routing for kernel 3 and the caller
-            a.ids[tid] = e;
-            a.wts[tid] = s_wts[t][j];
-            if (a.ids_out) a.ids_out[tid] = e;
-            if (a.wts_out) a.wts_out[tid] = s_wts[t][j];
-        }
+        a.ids[tid] = s_ids[t][j];
+        a.wts[tid] = s_wts[t][j];
+        if (a.ids_out) a.ids_out[tid] = s_ids[t][j];
+        if (a.wts_out) a.wts_out[tid] = s_wts[t][j];
     }
-    __syncthreads();
-    if (tid == 0) {  // the union: routed experts ascending, then the shared one
-        int n = 0;
-        for (int wd = 0; wd < (NE + 31) / 32; ++wd)
-            for (uint32_t m = bits[wd]; m; m &= m - 1) ulist[n++] = 32 * wd + __ffs(m) - 1;
-        if (a.NS > NU) ulist[n++] = -1;
-        s_nu = n;
-    }
+    if (w == 0) form_union(s_ids, T, NU, NE, a.NS > NU, s_flag, ulist, &s_nu);  // routed ascending, then the shared one
     __syncthreads();
     stamp(a, 3);
     const int units = s_nu * nbf, step = HALVES * gridDim.x;
@@ -244,8 +240,8 @@ __global__ void __launch_bounds__(512) k_fm_gate_up_unit(FArgs a) {
     constexpr bool Q8K = Fmt<TYPE>::Q8K;
     __shared__ int s_ids[FD_MAX_T][64];
     __shared__ float s_wts[FD_MAX_T][64];
-    __shared__ uint32_t bits[ROUTER_MAX_E / 32];
     __shared__ int ulist[FM_MAX_U], s_nu;
+    __shared__ __align__(4) uint8_t s_flag[ROUTER_MAX_E];
     __shared__ int s_slot[FD_MAX_T];
     __shared__ float gu[2][FD_MAX_T][32];  // [gate / up][token][row]
     __shared__ __align__(16) int8_t s_xq[FD_MAX_T * FD_MAX_E];
@@ -254,7 +250,6 @@ __global__ void __launch_bounds__(512) k_fm_gate_up_unit(FArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, gl = lane & (L_IN - 1), grp = lane / L_IN;
     const int T = a.T, FE = a.FE, NU = a.NU, NE = a.NE, nbf = FE / 32, nu_in = fmt_units(TYPE, a.E);
     stamp(a, 2);
-    for (int i = tid; i < (NE + 31) / 32; i += 512) bits[i] = 0u;
     const float* lg = a.logits_in ? a.logits_in : a.logits;
     if (w < T) {
         router_select_one_wave(lg + (size_t)w * NE, NE, NU, s_ids[w], s_wts[w]);
@@ -268,25 +263,14 @@ __global__ void __launch_bounds__(512) k_fm_gate_up_unit(FArgs a) {
             for (int i = i0; i < TE / 64; i += n) ((int4*)s_xbs)[i] = ((const int4*)a.xo.bsK)[i];
     }
     __syncthreads();
-    if (tid < T * NU) {
+    if (blockIdx.x == 0 && tid < T * NU) {  // the routing for kernel 3 and the caller
         const int t = tid / NU, j = tid - t * NU;
-        const int e = s_ids[t][j];
-        atomicOr(&bits[e >> 5], 1u << (e & 31));
-        if (blockIdx.x == 0) {  // the routing for kernel 3 and the caller
-            a.ids[tid] = e;
-            a.wts[tid] = s_wts[t][j];
-            if (a.ids_out) a.ids_out[tid] = e;
-            if (a.wts_out) a.wts_out[tid] = s_wts[t][j];
-        }
+        a.ids[tid] = s_ids[t][j];
+        a.wts[tid] = s_wts[t][j];
+        if (a.ids_out) a.ids_out[tid] = s_ids[t][j];
+        if (a.wts_out) a.wts_out[tid] = s_wts[t][j];
     }
-    __syncthreads();
-    if (tid == 0) {  // the union: routed experts ascending, then the shared one
-        int n = 0;
-        for (int wd = 0; wd < (NE + 31) / 32; ++wd)
-            for (uint32_t m = bits[wd]; m; m &= m - 1) ulist[n++] = 32 * wd + __ffs(m) - 1;
-        if (a.NS > NU) ulist[n++] = -1;
-        s_nu = n;
-    }
+    if (w == 0) form_union(s_ids, T, NU, NE, a.NS > NU, s_flag, ulist, &s_nu);  // routed ascending, then the shared one
     __syncthreads();
     stamp(a, 3);
     const int u = blockIdx.x / nbf, b = blockIdx.x - u * nbf;
