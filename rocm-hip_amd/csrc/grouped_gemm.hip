@@ -161,10 +161,9 @@ struct HBuf {  // FP4 types
     float dx[KB / 4][GG_TILE][4];
 };
 template <int NM, int KB>
-struct KBuf {  // Q4_K: one stage = one (KB = 4) or two (KB = 8) 128-value halves of a super-block
-    uint8_t a[NM][4][KB][1024];      // [matrix][wave][sub-block][lane * 16]: 12-byte FP6 slots
+struct KBuf {  // Q4_K: one stage = one (KB = 4) or two (KB = 8) 128-value halves of a super-block (weights: registers)
     uint8_t b[KB][GG_NT][2][1024];   // [sub-block][entry tile][16-value half][lane * 16]: FP16 activations
-    _Float16 bs[GG_TILE][2 * KB];    // [entry][16-value sum of the stage]: Q8_K sums of 16 as FP16
+    float bd[GG_TILE][KB];           // [entry][sub-block]: its sum of 32 Q8_K values times the entry's scale
     float dx[GG_TILE];               // [entry]: the Q8_K scale of the stage's super-block
 };
 template <int TYPE, int NM, int KB>
@@ -176,8 +175,12 @@ struct BufOf {
 #endif
 #define KQ GG_KBQ4
 template <int NM, int KB>
+struct KBuf2 {  // Q4_K: two stages, one being computed while the next one's loads land
+    KBuf<NM, KB> s[2];
+};
+template <int NM, int KB>
 struct BufOf<QT_Q4_K, NM, KB> {
-    typedef KBuf<NM, KQ> type;
+    typedef KBuf2<NM, KQ> type;
 };
 template <int NM, int KB>
 struct BufOf<QT_ROCMFP4, NM, KB> {
@@ -355,11 +358,12 @@ __device__ __forceinline__ void h_compute(const HBuf<NM, KB>& B, const uint4 (&w
 //   isum = sum_j sc_j . sum_{i in j} q_i qx_i   on eight f16 MFMAs with A = sc_j q (the FP6 codes decoded with the
 //          factor 2, times the FP16 sub-block scale: integers <= 945, exact), B = qx (Q8_K values, exact): every
 //          partial sum an integer below 945 x 127 x 128 < 2^24, so exact in fp32 in any order;
-//   msum = sum_j m_j (bs_2j + bs_2j+1)         on one 32 x 32 x 8 f16 MFMA (mins <= 63, sums of 16 <= 2032: exact);
-//   acc += dx (d isum - dmin msum)            d, dmin per row (FP16, broadcast by an outer-product MFMA), dx the
-//                                              entry's Q8_K scale: three VALU operations per output and 128 values.
+//   acc += (d dx) isum                         S = d (x) dx, the row's FP16 d times the entry's Q8_K scale, from an
+//                                              outer-product f32 MFMA (one rounding), then one VALU FMA per output;
+//   acc -= sum_j (dmin m_j) (bsum_j dx)        two f32 MFMAs accumulating into acc: A = -dmin m_j (exact in fp32),
+//                                              B = bsum_j dx, bsum_j the sub-block's sum of 32 Q8_K values.
 // The reference's K-quant WMMA kernel forms the same integer sums per 128-value chunk (src/matvec_q.hip:2952-3008)
-// and the same float step.
+// and the same float step (d isum - dmin msum) dx, in another fp32 order.
 struct KSc2 {  // a lane's row scales for a 128-value half: sc_4c..sc_4c+3 and m_4c..m_4c+3 as FP16
     uint2 sc, m;
 };
@@ -369,17 +373,25 @@ struct KSc {  // ... for a stage of KB / 4 halves, and the super-block's (d, dmi
     uint32_t dd;
 };
 
-template <int NM, int KB>
-__device__ __forceinline__ void k_issue(KBuf<NM, KB>& B, int b0, KSc<KB>& ks, const uint8_t* vt, const uint8_t* sct,
-                                        const int8_t* xu, int xs, uint4 (&xb)[KB / 2], int4& bsv, float& dxv,
-                                        const int* bsr, const float* dxr, int w, int tid) {
+// Issue one stage's loads, all into registers: the wave's weight codes (12 bytes a lane per sub-block, one
+// contiguous 768-byte run per load) and rows' scales; and the activations of the wave's 16 entries 16 w + l % 16,
+// lanes l / 16 reading consecutive 16-byte units of each entry's run of the stage, so that one load touches 16
+// entries' 64-byte pieces (a lane per entry, as the other kernels stage them, makes every load touch 64 rows):
+// unit c = 4 j + l / 16 of the stage (sub-block c / 2, 16-value half c % 2), the sums of 16 of sub-blocks
+// l / 16 + 4 q (a pair each) and the entry's scale. xu, bsr, dxr: the lane's entry row's values (+ 16 (l / 16)),
+// sums of 16 (+ 2 (l / 16)) and scales.
+template <int KB>
+__device__ __forceinline__ void k_issue(int b0, uint3 (&wv)[KB], KSc<KB>& ks, const uint8_t* vt, const uint8_t* sct,
+                                        const int8_t* xu, uint4 (&xb)[KB / 2], int2 (&bsv)[KB / 4], float& dxv,
+                                        const int* bsr, const float* dxr) {
     static_assert(KB == 4 || KB == 8, "a Q4_K stage is one or two 128-value halves of a super-block");
 #pragma unroll
-    for (int c = 0; c < KB; ++c) lds_load12(vt + 768 * (b0 + c), B.a[0][w][c]);
+    for (int c = 0; c < KB; ++c) wv[c] = *(const uint3*)(vt + 768 * (b0 + c));
 #pragma unroll
-    for (int j = 0; j < KB / 2; ++j) xb[j] = *(const uint4*)(xu + xs * (b0 + (tid >> 7) + 2 * j));
-    if (tid < 32 * KB) bsv = *(const int4*)(bsr + 2 * b0);  // entry tid % 64, sums 4 (tid / 64) .. + 3 of the stage
-    if (KB == 8 ? tid < 64 : (tid >= 128 && tid < 192)) dxv = dxr[b0 >> 3];  // entry tid % 64
+    for (int j = 0; j < KB / 2; ++j) xb[j] = *(const uint4*)(xu + 32 * b0 + 64 * j);
+#pragma unroll
+    for (int q = 0; q < KB / 4; ++q) bsv[q] = *(const int2*)(bsr + 2 * b0 + 8 * q);
+    dxv = dxr[b0 >> 3];
     const uint8_t* slot = sct + Q4K_TILE_SLOT * 32 * (b0 >> 3);
     if constexpr (KB == 8) {
         const uint4 sc = *(const uint4*)slot, m = *(const uint4*)(slot + 16);
@@ -392,39 +404,54 @@ __device__ __forceinline__ void k_issue(KBuf<NM, KB>& B, int b0, KSc<KB>& ks, co
     ks.dd = *(const uint32_t*)(slot + 32);
 }
 
+// (v_fence: the value is taken as changed here, so that the compiler neither hoists the conversions that use it
+// above this point, next to the loads issued a stage earlier, nor waits for those loads before it)
+__device__ __forceinline__ void v_fence(uint32_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void v_fence(float& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void v_fence(uint2& v) { asm volatile("" : "+v"(v.x), "+v"(v.y)); }
+__device__ __forceinline__ void v_fence(int2& v) { asm volatile("" : "+v"(v.x), "+v"(v.y)); }
+__device__ __forceinline__ void v_fence(uint3& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z)); }
+__device__ __forceinline__ void v_fence(uint4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
+
+// The stage's activations into the FP16 operand runs (values 0..7 of a unit to the slot of (entry, K half 0) of its
+// sub-block's run for its 16-value half, values 8..15 to that of (entry, K half 1): the 16 lanes of one unit write
+// 16 consecutive slots), each sub-block's sum of 32 values times the entry's scale, and the scale
 template <int NM, int KB>
-__device__ __forceinline__ void k_stage(KBuf<NM, KB>& B, const uint4 (&xb)[KB / 2], const int4& bsv, float dxv,
-                                        int tid) {
-    h_stage_b<NM, KB>(B, xb, tid);
-    if (tid < 32 * KB) {
-        const h2 lo = {(_Float16)bsv.x, (_Float16)bsv.y}, hi = {(_Float16)bsv.z, (_Float16)bsv.w};  // exact
-        *(uint2*)&B.bs[tid & 63][4 * (tid >> 6)] = make_uint2(__builtin_bit_cast(uint32_t, lo),
-                                                               __builtin_bit_cast(uint32_t, hi));
+__device__ __forceinline__ void k_stage(KBuf<NM, KB>& B, uint4 (&xb)[KB / 2], int2 (&bsv)[KB / 4], float& dxv,
+                                        int w, int l) {
+#pragma unroll
+    for (int j = 0; j < KB / 2; ++j) v_fence(xb[j]);
+#pragma unroll
+    for (int q = 0; q < KB / 4; ++q) v_fence(bsv[q]);
+    v_fence(dxv);
+    const int e = 16 * w + (l & 15), u = l >> 4;
+#pragma unroll
+    for (int j = 0; j < KB / 2; ++j) {
+        const int c = 4 * j + u;
+        uint8_t* run = B.b[c >> 1][e >> 5][c & 1];
+        *(uint4*)(run + 16 * (e & 31)) = i8x8_to_f16(xb[j].x, xb[j].y);
+        *(uint4*)(run + 16 * (32 + (e & 31))) = i8x8_to_f16(xb[j].z, xb[j].w);
     }
-    if (KB == 8 ? tid < 64 : (tid >= 128 && tid < 192)) B.dx[tid & 63] = dxv;
+#pragma unroll
+    for (int q = 0; q < KB / 4; ++q) B.bd[e][u + 4 * q] = (float)(bsv[q].x + bsv[q].y) * dxv;  // (the sum: exact)
+    if (u == 0) B.dx[e] = dxv;
 }
 
 template <int NM, int KB, int NTU>
-__device__ __forceinline__ void k_compute(const KBuf<NM, KB>& B, const KSc<KB>& ks, v16f (&acc)[NM][NTU], int w,
-                                          int l, int lr, int kh) {
+__device__ __forceinline__ void k_compute(const KBuf<NM, KB>& B, const uint3 (&wv)[KB], const KSc<KB>& ks,
+                                          v16f (&acc)[NM][NTU], int l, int lr, int kh) {
     const v16f z = {};
-    // D[j] = d, Dm[j] = dmin of the lane's row 8 (j / 4) + 4 kh + j % 4: outer products with ones (exact)
-    const _Float16 one = kh ? (_Float16)0.0f : (_Float16)1.0f;
     const h2 dd = __builtin_bit_cast(h2, ks.dd);
-    const v4h ad = {kh ? (_Float16)0.0f : dd.x, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
-    const v4h adm = {kh ? (_Float16)0.0f : dd.y, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
-    const v4h b1 = {one, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
-    const v16f D = __builtin_amdgcn_mfma_f32_32x32x8f16(ad, b1, z, 0, 0, 0);
-    const v16f Dm = __builtin_amdgcn_mfma_f32_32x32x8f16(adm, b1, z, 0, 0, 0);
+    const float aD = kh ? 0.0f : (float)dd.x;  // S's A: the lane's row's d in k = 0
+    const float ndm = -(float)dd.y;
 #pragma unroll
-    for (int hc = 0; hc < KB / 4; ++hc) {  // each 128-value half: its integer sums, then one float step
+    for (int hc = 0; hc < KB / 4; ++hc) {  // each 128-value half: its integer sums, then the float steps
         const KSc2& kh2 = ks.h[hc];
         // A of the half's four sub-blocks: codes decoded two sub-blocks at a time, times the sub-block's scale
         v8h A0[4], A1[4];
 #pragma unroll
         for (int bp = 0; bp < 4; bp += 2) {
-            const uint3 c0 = *(const uint3*)(B.a[0][w][4 * hc + bp] + 16 * l);
-            const uint3 c1 = *(const uint3*)(B.a[0][w][4 * hc + bp + 1] + 16 * l);
+            const uint3 c0 = wv[4 * hc + bp], c1 = wv[4 * hc + bp + 1];
             const v32h d =
                 __builtin_amdgcn_cvt_scalef32_pk32_f16_fp6((v6u){c0.x, c0.y, c0.z, c1.x, c1.y, c1.z}, 2.0f);
 #pragma unroll
@@ -436,10 +463,9 @@ __device__ __forceinline__ void k_compute(const KBuf<NM, KB>& B, const KSc<KB>& 
                 A1[jj] = scaled8(d, 2 * kk + 1, sc);
             }
         }
-        // M's A: k = 4 kh .. 4 kh + 3 hold m of sub-blocks 2 kh, 2 kh, 2 kh + 1, 2 kh + 1 (each against a sum of 16)
-        const uint32_t mw = kh ? kh2.m.y : kh2.m.x;
-        const v4h Am = __builtin_bit_cast(v4h, make_uint2(__builtin_amdgcn_perm(mw, mw, 0x01000100u),
-                                                           __builtin_amdgcn_perm(mw, mw, 0x03020302u)));
+        // the mins' A: k = kh of the first MFMA is sub-block kh, of the second sub-block 2 + kh
+        const float am0 = ndm * (float)__builtin_bit_cast(h2, kh2.m.x)[kh];
+        const float am1 = ndm * (float)__builtin_bit_cast(h2, kh2.m.y)[kh];
 #pragma unroll
         for (int t = 0; t < NTU; ++t) {
             v16f P = z;
@@ -450,14 +476,13 @@ __device__ __forceinline__ void k_compute(const KBuf<NM, KB>& B, const KSc<KB>& 
                 P = __builtin_amdgcn_mfma_f32_32x32x16_f16(
                     A1[jj], B1, __builtin_amdgcn_mfma_f32_32x32x16_f16(A0[jj], B0, P, 0, 0, 0), 0, 0, 0);
             }
-            const v4h Bm = *(const v4h*)&B.bs[32 * t + lr][8 * hc + 4 * kh];
-            const v16f M = __builtin_amdgcn_mfma_f32_32x32x8f16(Am, Bm, z, 0, 0, 0);
-            const float dxv = B.dx[32 * t + lr];
+            const float* bd = B.bd[32 * t + lr];
+            const float bdx = kh ? 0.0f : B.dx[32 * t + lr];
+            const v16f S = __builtin_amdgcn_mfma_f32_32x32x2f32(aD, bdx, z, 0, 0, 0);
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const float mm = Dm[j] * M[j];
-                acc[0][t][j] = fmaf(fmaf(D[j], P[j], -mm), dxv, acc[0][t][j]);
-            }
+            for (int j = 0; j < 16; ++j) acc[0][t][j] = fmaf(P[j], S[j], acc[0][t][j]);
+            acc[0][t] = __builtin_amdgcn_mfma_f32_32x32x2f32(am0, bd[4 * hc + kh], acc[0][t], 0, 0, 0);
+            acc[0][t] = __builtin_amdgcn_mfma_f32_32x32x2f32(am1, bd[4 * hc + 2 + kh], acc[0][t], 0, 0, 0);
         }
     }
 }
@@ -475,12 +500,15 @@ template <int TYPE, int NM, int KB>
 #ifndef GG_WPE
 #define GG_WPE 3  // waves per SIMD asked of the compiler (0: its choice; 3 measured 3-8% faster than its 2)
 #endif
+#ifndef GG_WPE_Q4K
+#define GG_WPE_Q4K 2  // the Q4_K kernel: its stage loads in flight during the previous stage's compute take registers
+#endif
 #ifndef GG_WPE_D8
 #define GG_WPE_D8 5  // the same for the one-matrix Q8_0 kernel (96 VGPRs: five workgroups per CU; 6 spilled, config 2 +13%)
 #endif
 __global__ void __launch_bounds__(256)
 #if GG_WPE
-__attribute__((amdgpu_waves_per_eu(TYPE == QT_Q8_0 && NM == 1 ? GG_WPE_D8 : GG_WPE)))
+__attribute__((amdgpu_waves_per_eu(TYPE == QT_Q8_0 && NM == 1 ? GG_WPE_D8 : TYPE == QT_Q4_K ? GG_WPE_Q4K : GG_WPE)))
 #endif
 k_grouped(GArgs a) {
     __shared__ __attribute__((aligned(1024))) typename BufOf<TYPE, NM, KB>::type buf;
@@ -560,24 +588,48 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
     const int nst = nb / KB;
     if constexpr (Q4K) {
         static_assert(NM == 1, "Q4_K: one matrix a launch (down's Q8_K input is quantized per 256 values)");
-        const int ue = tid & 63, uh = (tid >> 6) & 1;
-        const int8_t* xu = a.xq + (long long)in_row(min(ue, cnt - 1)) * K + 16 * uh;
-        // the entry whose sums of 16 (threads 0..127) or scale (threads 128..191) this thread stages
-        const long long br = in_row(min(tid & 63, cnt - 1));
-        const int* bsr = a.xbs + br * (K / 16) + 4 * ((tid >> 6) & (KQ / 2 - 1));
+        // this lane's entry 16 w + l % 16 (the last one for lanes past the tile's entries) and unit l / 16
+        const long long br = in_row(min(16 * w + (l & 15), cnt - 1));
+        const int8_t* xu = a.xq + br * K + 16 * (l >> 4);
+        const int* bsr = a.xbs + br * (K / 16) + 2 * (l >> 4);
         const float* kdr = a.xd + br * (K / 256);
-        KSc<KQ> ks;
+        // Software-pipelined over the two stage buffers: stage s + 1's loads are issued after the barrier that
+        // publishes stage s and land while stage s is computed; one barrier per stage (a wave past it has finished
+        // computing stage s - 1, whose buffer the loads then reuse). The stage count nb / KQ is even (K % 256 == 0).
+        KSc<KQ> ksn;
+        uint3 wvn[KQ];
         uint4 xb[KQ / 2];
-        int4 bsv = {};
-        float dxv = 0.0f;
-        for (int s = 0; s < nb / KQ; ++s) {
-            k_issue<NM, KQ>(buf, s * KQ, ks, vt[0], sct[0], xu, 32, xb, bsv, dxv, bsr, kdr, w, tid);
-            wait_vm<0>();
-            k_stage<NM, KQ>(buf, xb, bsv, dxv, tid);
+        int2 bsv[KQ / 4];
+        float dxv;
+        const int ns = nb / KQ;
+        k_issue<KQ>(0, wvn, ksn, vt[0], sct[0], xu, xb, bsv, dxv, bsr, kdr);
+        auto step = [&](KBuf<NM, KQ>& cur, int s) {
+            k_stage<NM, KQ>(cur, xb, bsv, dxv, w, l);
+            KSc<KQ> ks = ksn;
+            uint3 wv[KQ];
+#pragma unroll
+            for (int c = 0; c < KQ; ++c) {
+                wv[c] = wvn[c];
+                v_fence(wv[c]);
+            }
+#pragma unroll
+            for (int h = 0; h < KQ / 4; ++h) {
+                v_fence(ks.h[h].sc);
+                v_fence(ks.h[h].m);
+            }
+            v_fence(ks.dd);
             __syncthreads();
-            k_compute<NM, KQ, NTU>(buf, ks, acc, w, l, lr, kh);
-            __syncthreads();
+            // (the last stage loads itself again, from L2: an unconditional issue keeps every stage's registers
+            // in one place, where a skipped one would make the compiler copy them and wait for the loads)
+            k_issue<KQ>(min(s + 1, ns - 1) * KQ, wvn, ksn, vt[0], sct[0], xu, xb, bsv, dxv, bsr, kdr);
+            k_compute<NM, KQ, NTU>(cur, wv, ks, acc, l, lr, kh);
+            __builtin_amdgcn_sched_barrier(0);  // (the next stage's staging stays after this compute)
+        };
+        for (int s = 0; s < ns; s += 2) {
+            step(buf.s[0], s);
+            step(buf.s[1], s + 1);
         }
+        __syncthreads();  // (the output transpose below reuses the buffers)
     } else if constexpr (!F16) {
         // this lane's activation run: entry 32 (w % GG_NT) + lr, K half kh
         const int8_t* xrow;
