@@ -178,10 +178,13 @@ __global__ void __launch_bounds__(256) k_pack(const uint8_t* W, long long row_by
 //   Q8_0:      16-byte slots: the block's int8 values 16 h .. 16 h + 15 (the int8 MFMA's A);
 //   FP4 types: 12-byte slots: the block's values 8 h .. 8 h + 7, then 16 + 8 h .. + 7 (the f16 MFMAs' A of each
 //              16-value half), each as the FP6 E2M3 code of codebook value / 2, 6 bits per value from bit 0 up.
-//   Q4_K:      the same 12-byte slots per 32-value sub-block, each code the FP6 E2M3 of quant / 2 (quant 0..15).
+//   Q4_K:      the same 12-byte slots per 32-value sub-block, each code the FP6 E2M3 of quant / 2 (quant 0..15),
+//              stage-major: the four slots of a lane for sub-blocks 4 s .. 4 s + 3 as 48 contiguous bytes, split in
+//              three 16-byte chunks, chunk i at 1024 i + 16 l of the stage's 3 KB (three coalesced loads a stage).
 // Scale tiles, per group g and 8-block group q (Q4_K: super-block), 32 row slots: Q8_0 16 bytes (8 blocks' FP16 d);
-// FP4 types 32 bytes (per block the FP16 pair (e0, e1) of its UE4M3 half-scales, FAST (e, e)); Q4_K 48 bytes (the
-// sub-block scales sc0..sc7 as FP16, the mins m0..m7 as FP16, then the FP16 d and dmin and 12 zero bytes).
+// FP4 types 32 bytes (per block the FP16 pair (e0, e1) of its UE4M3 half-scales, FAST (e, e)); Q4_K 32 bytes, 16
+// per 128-value half c: the sub-block scales sc_4c..sc_4c+3 and mins m_4c..m_4c+3 as bytes, the FP16 d and dmin,
+// 4 zero bytes.
 __device__ __forceinline__ uint32_t fp4_code(const uint8_t* qs, int v) {  // code of value v (0..31) of a block
     return v < 16 ? (qs[v] & 0x0fu) : (qs[v - 16] >> 4);
 }
@@ -219,6 +222,8 @@ __global__ void __launch_bounds__(256) k_pack_tiles(const uint8_t* W, long long 
         // the native block holding block b (Q4_K: super-block b / 8, of which b is sub-block b % 8)
         const uint8_t* blk = W + (32 * g + (l & 31)) * row_bytes + (long long)(TYPE == QT_Q4_K ? b >> 3 : b) * BB;
         uint8_t* dst = V + SS * i;
+        if constexpr (TYPE == QT_Q4_K)  // stage-major: byte p of the lane's 48 for the stage (4 sub-blocks)
+            dst = V + (long long)g * nb * 768 + 3072 * (b >> 2) + 16 * l;
         if constexpr (TYPE == QT_Q8_0) {
             for (int j = 0; j < 16; ++j) dst[j] = blk[2 + 16 * h + j];
         } else {
@@ -234,7 +239,10 @@ __global__ void __launch_bounds__(256) k_pack_tiles(const uint8_t* W, long long 
                 w[bit >> 5] |= f << (bit & 31);
                 if ((bit & 31) > 26) w[(bit >> 5) + 1] |= f >> (32 - (bit & 31));
             }
-            for (int j = 0; j < 12; ++j) dst[j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+            for (int j = 0; j < 12; ++j) {
+                const int p = TYPE == QT_Q4_K ? 12 * (b & 3) + j : j;
+                dst[TYPE == QT_Q4_K ? 1024 * (p >> 4) + (p & 15) : j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+            }
         }
         return;
     }
@@ -246,22 +254,22 @@ __global__ void __launch_bounds__(256) k_pack_tiles(const uint8_t* W, long long 
     const uint8_t* row = W + r * row_bytes;
     constexpr int SB = TYPE == QT_Q8_0 ? 16 : TYPE == QT_Q4_K ? Q4K_TILE_SLOT : 32;  // slot bytes
     uint8_t* dst = S + ((r / 32) * nq + q) * (32 * SB) + (r & 31) * SB;
-    if constexpr (TYPE == QT_Q4_K) {  // super-block q: sc0..sc7, m0..m7 as FP16 (exact: 6-bit integers), d, dmin
+    if constexpr (TYPE == QT_Q4_K) {  // super-block q, per half c: sc_4c..+3, m_4c..+3 (bytes), d, dmin, zeros
         const uint8_t* blk = row + (long long)q * BB;
         uint32_t sw[3];
         for (int j = 0; j < 3; ++j)
             sw[j] = (uint32_t)blk[4 + 4 * j] | (uint32_t)blk[5 + 4 * j] << 8 | (uint32_t)blk[6 + 4 * j] << 16 |
                     (uint32_t)blk[7 + 4 * j] << 24;
-        uint16_t* o = (uint16_t*)dst;
         for (int j = 0; j < 8; ++j) {
             int sc, mn;
             q4k_scale_min(j, sw, sc, mn);
-            o[j] = __half_as_ushort(__float2half((float)sc));
-            o[8 + j] = __half_as_ushort(__float2half((float)mn));
+            dst[16 * (j >> 2) + (j & 3)] = (uint8_t)sc;
+            dst[16 * (j >> 2) + 4 + (j & 3)] = (uint8_t)mn;
         }
-        o[16] = (uint16_t)(blk[0] | blk[1] << 8);  // d
-        o[17] = (uint16_t)(blk[2] | blk[3] << 8);  // dmin
-        for (int j = 18; j < 24; ++j) o[j] = 0;
+        for (int c = 0; c < 2; ++c) {
+            for (int j = 0; j < 4; ++j) dst[16 * c + 8 + j] = blk[j];  // d, dmin (FP16)
+            for (int j = 12; j < 16; ++j) dst[16 * c + j] = 0;
+        }
         return;
     }
     for (int b = 0; b < 8; ++b) {

@@ -364,13 +364,9 @@ __device__ __forceinline__ void h_compute(const HBuf<NM, KB>& B, const uint4 (&w
 //                                              B = bsum_j dx, bsum_j the sub-block's sum of 32 Q8_K values.
 // The reference's K-quant WMMA kernel forms the same integer sums per 128-value chunk (src/matvec_q.hip:2952-3008)
 // and the same float step (d isum - dmin msum) dx, in another fp32 order.
-struct KSc2 {  // a lane's row scales for a 128-value half: sc_4c..sc_4c+3 and m_4c..m_4c+3 as FP16
-    uint2 sc, m;
-};
 template <int KB>
-struct KSc {  // ... for a stage of KB / 4 halves, and the super-block's (d, dmin)
-    KSc2 h[KB / 4];
-    uint32_t dd;
+struct KSc {  // a lane's row scales for each 128-value half of a stage: its tile record (sc_j and m_j as bytes, d, dmin)
+    uint4 h[KB / 4];
 };
 
 // Issue one stage's loads, all into registers: the wave's weight codes (12 bytes a lane per sub-block, one
@@ -381,27 +377,20 @@ struct KSc {  // ... for a stage of KB / 4 halves, and the super-block's (d, dmi
 // l / 16 + 4 q (a pair each) and the entry's scale. xu, bsr, dxr: the lane's entry row's values (+ 16 (l / 16)),
 // sums of 16 (+ 2 (l / 16)) and scales.
 template <int KB>
-__device__ __forceinline__ void k_issue(int b0, uint3 (&wv)[KB], KSc<KB>& ks, const uint8_t* vt, const uint8_t* sct,
-                                        const int8_t* xu, uint4 (&xb)[KB / 2], int2 (&bsv)[KB / 4], float& dxv,
-                                        const int* bsr, const float* dxr) {
+__device__ __forceinline__ void k_issue(int b0, uint4 (&wv)[3 * KB / 4], KSc<KB>& ks, const uint8_t* vt,
+                                        const uint8_t* sct, const int8_t* xu, uint4 (&xb)[KB / 2],
+                                        int2 (&bsv)[KB / 4], float& dxv, const int* bsr, const float* dxr) {
     static_assert(KB == 4 || KB == 8, "a Q4_K stage is one or two 128-value halves of a super-block");
 #pragma unroll
-    for (int c = 0; c < KB; ++c) wv[c] = *(const uint3*)(vt + 768 * (b0 + c));
+    for (int c = 0; c < 3 * KB / 4; ++c) wv[c] = *(const uint4*)(vt + 768 * b0 + 1024 * c);
 #pragma unroll
     for (int j = 0; j < KB / 2; ++j) xb[j] = *(const uint4*)(xu + 32 * b0 + 64 * j);
 #pragma unroll
     for (int q = 0; q < KB / 4; ++q) bsv[q] = *(const int2*)(bsr + 2 * b0 + 8 * q);
     dxv = dxr[b0 >> 3];
-    const uint8_t* slot = sct + Q4K_TILE_SLOT * 32 * (b0 >> 3);
-    if constexpr (KB == 8) {
-        const uint4 sc = *(const uint4*)slot, m = *(const uint4*)(slot + 16);
-        ks.h[0] = {make_uint2(sc.x, sc.y), make_uint2(m.x, m.y)};
-        ks.h[1] = {make_uint2(sc.z, sc.w), make_uint2(m.z, m.w)};
-    } else {
-        const int c = (b0 >> 2) & 1;
-        ks.h[0] = {*(const uint2*)(slot + 8 * c), *(const uint2*)(slot + 16 + 8 * c)};
-    }
-    ks.dd = *(const uint32_t*)(slot + 32);
+    const uint8_t* slot = sct + Q4K_TILE_SLOT * 32 * (b0 >> 3) + 16 * ((b0 >> 2) & 1);
+#pragma unroll
+    for (int h = 0; h < KB / 4; ++h) ks.h[h] = *(const uint4*)(slot + 16 * h);
 }
 
 // (v_fence: the value is taken as changed here, so that the compiler neither hoists the conversions that use it
@@ -437,35 +426,47 @@ __device__ __forceinline__ void k_stage(KBuf<NM, KB>& B, uint4 (&xb)[KB / 2], in
     if (u == 0) B.dx[e] = dxv;
 }
 
+// (sc, sc) as an FP16 pair for sub-block j's scale byte in w: the byte under FP16 1024's exponent is 1024 + sc
+__device__ __forceinline__ uint32_t sc_pair(uint32_t w, int j) {
+    const h2 v = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w, 0x04000400u | (0x00010001u * j)));
+    return __builtin_bit_cast(uint32_t, v - (h2){(_Float16)1024.0f, (_Float16)1024.0f});
+}
+
 template <int NM, int KB, int NTU>
-__device__ __forceinline__ void k_compute(const KBuf<NM, KB>& B, const uint3 (&wv)[KB], const KSc<KB>& ks,
+__device__ __forceinline__ void k_compute(const KBuf<NM, KB>& B, const uint4 (&wv)[3 * KB / 4], const KSc<KB>& ks,
                                           v16f (&acc)[NM][NTU], int l, int lr, int kh) {
     const v16f z = {};
-    const h2 dd = __builtin_bit_cast(h2, ks.dd);
-    const float aD = kh ? 0.0f : (float)dd.x;  // S's A: the lane's row's d in k = 0
-    const float ndm = -(float)dd.y;
+    uint32_t wd[3 * KB];  // the lane's codes: 3 dwords (16 FP6 codes) per sub-block
+#pragma unroll
+    for (int c = 0; c < 3 * KB / 4; ++c) {
+        wd[4 * c] = wv[c].x;
+        wd[4 * c + 1] = wv[c].y;
+        wd[4 * c + 2] = wv[c].z;
+        wd[4 * c + 3] = wv[c].w;
+    }
 #pragma unroll
     for (int hc = 0; hc < KB / 4; ++hc) {  // each 128-value half: its integer sums, then the float steps
-        const KSc2& kh2 = ks.h[hc];
+        const uint4 r = ks.h[hc];
+        const h2 dd = __builtin_bit_cast(h2, r.z);
+        const float aD = kh ? 0.0f : (float)dd.x;  // S's A: the lane's row's d in k = 0
+        const float ndm = -(float)dd.y;
         // A of the half's four sub-blocks: codes decoded two sub-blocks at a time, times the sub-block's scale
         v8h A0[4], A1[4];
 #pragma unroll
         for (int bp = 0; bp < 4; bp += 2) {
-            const uint3 c0 = wv[4 * hc + bp], c1 = wv[4 * hc + bp + 1];
-            const v32h d =
-                __builtin_amdgcn_cvt_scalef32_pk32_f16_fp6((v6u){c0.x, c0.y, c0.z, c1.x, c1.y, c1.z}, 2.0f);
+            const uint32_t* c = wd + 12 * hc + 3 * bp;
+            const v32h d = __builtin_amdgcn_cvt_scalef32_pk32_f16_fp6((v6u){c[0], c[1], c[2], c[3], c[4], c[5]}, 2.0f);
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
                 const int jj = bp + kk;
-                const uint32_t scw = jj < 2 ? kh2.sc.x : kh2.sc.y;
-                const uint32_t sc = __builtin_amdgcn_perm(scw, scw, (jj & 1) ? 0x03020302u : 0x01000100u);  // (sc, sc)
+                const uint32_t sc = sc_pair(r.x, jj);
                 A0[jj] = scaled8(d, 2 * kk, sc);
                 A1[jj] = scaled8(d, 2 * kk + 1, sc);
             }
         }
-        // the mins' A: k = kh of the first MFMA is sub-block kh, of the second sub-block 2 + kh
-        const float am0 = ndm * (float)__builtin_bit_cast(h2, kh2.m.x)[kh];
-        const float am1 = ndm * (float)__builtin_bit_cast(h2, kh2.m.y)[kh];
+        // the mins' A: k = kh of the first MFMA is sub-block kh, of the second sub-block 2 + kh (exact products)
+        const float am0 = ndm * (float)((r.y >> (8 * kh)) & 0xffu);
+        const float am1 = ndm * (float)((r.y >> (16 + 8 * kh)) & 0xffu);
 #pragma unroll
         for (int t = 0; t < NTU; ++t) {
             v16f P = z;
@@ -568,7 +569,7 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
     const long long grp = ((long long)e * a.N + r0) / 32;
     constexpr bool Q4K = TYPE == QT_Q4_K;
     constexpr int SB = Q4K ? Q4K_TILE_SLOT : F16 ? 32 : 16;
-    constexpr int VS = F16 ? 12 : 16;  // value slot bytes
+    constexpr int VS = F16 && !Q4K ? 12 : 16;  // value slot bytes (Q4_K: a lane's 16-byte chunk of its stage)
     const uint8_t* vt[NM];
     const uint8_t* sct[NM];
     vt[0] = (shk ? a.vs : a.v) + grp * a.vrb + VS * l;
@@ -597,7 +598,7 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
         // publishes stage s and land while stage s is computed; one barrier per stage (a wave past it has finished
         // computing stage s - 1, whose buffer the loads then reuse). The stage count nb / KQ is even (K % 256 == 0).
         KSc<KQ> ksn;
-        uint3 wvn[KQ];
+        uint4 wvn[3 * KQ / 4];
         uint4 xb[KQ / 2];
         int2 bsv[KQ / 4];
         float dxv;
@@ -606,18 +607,14 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
         auto step = [&](KBuf<NM, KQ>& cur, int s) {
             k_stage<NM, KQ>(cur, xb, bsv, dxv, w, l);
             KSc<KQ> ks = ksn;
-            uint3 wv[KQ];
+            uint4 wv[3 * KQ / 4];
 #pragma unroll
-            for (int c = 0; c < KQ; ++c) {
+            for (int c = 0; c < 3 * KQ / 4; ++c) {
                 wv[c] = wvn[c];
                 v_fence(wv[c]);
             }
 #pragma unroll
-            for (int h = 0; h < KQ / 4; ++h) {
-                v_fence(ks.h[h].sc);
-                v_fence(ks.h[h].m);
-            }
-            v_fence(ks.dd);
+            for (int h = 0; h < KQ / 4; ++h) v_fence(ks.h[h]);
             __syncthreads();
             // (the last stage loads itself again, from L2: an unconditional issue keeps every stage's registers
             // in one place, where a skipped one would make the compiler copy them and wait for the loads)

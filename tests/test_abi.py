@@ -158,10 +158,10 @@ def test_caller_built_on_the_reference_headers_links_and_runs(tmp_path):
 
 def test_registered_bytes_per_mode():
     """Device bytes a registration allocates besides W: the copy (native size) unless in place, the tiles (Q8_0: the
-    native size; FP4: 0.75 K + K / 8 bytes per row; Q4_K: 0.75 K + 48 bytes per super-block) unless left out."""
+    native size; FP4: 0.75 K + K / 8 bytes per row; Q4_K: 0.75 K + 32 bytes per super-block) unless left out."""
     lib = moe_hip.load_library()
     rows, K = 128 * 768, 2048
-    for t, rb, tile_row in ((8, 2176, 2048 + 128), (100, 1152, 1536 + 256), (12, 1152, 1536 + 8 * 48)):
+    for t, rb, tile_row in ((8, 2176, 2048 + 128), (100, 1152, 1536 + 256), (12, 1152, 1536 + 8 * 32)):
         native = rows * rb
         assert lib.qmatvec_registered_bytes(t, rows, K, 0) == native + rows * tile_row
         assert lib.qmatvec_registered_bytes(t, rows, K, 1) == rows * tile_row
