@@ -117,16 +117,17 @@ __device__ __forceinline__ void acc_block(v16f& acc, const v16i& I, const v16f& 
     for (int j = 0; j < 16; ++j) acc[j] = fmaf((float)I[j], S[j], acc[j]);
 }
 
-// ---- Pipeline. K runs in stages of KB blocks through one LDS buffer per workgroup. Weight tiles, activation
-// scales and (Q8_0 kernel) activations move from memory to LDS with global_load_lds_dwordx4: lane l of such a load
-// writes its 16 bytes to slot l of a 1 KB LDS run, so each run is read back as an MFMA operand with one ds_read per
-// lane. The FP4 kernel stages its activations through registers instead (converted to FP16 on the way). The weight
-// rows' scales come through registers.
+// ---- Pipeline. Q8_0 and FP4: K runs in stages of KB blocks through one LDS buffer per workgroup. Weight tiles,
+// activation scales and (Q8_0 kernel) activations move from memory to LDS with global_load_lds_dwordx4: lane l of
+// such a load writes its 16 bytes to slot l of a 1 KB LDS run, so each run is read back as an MFMA operand with one
+// ds_read per lane. The FP4 kernel stages its activations through registers instead (converted to FP16 on the
+// way). The weight rows' scales come through registers. Q4_K (below) loads everything into registers one stage
+// ahead and stages its activations into two LDS buffers in turn.
 typedef __attribute__((address_space(3))) void lds_void;
 #ifndef GG_WNT
-#define GG_WNT 0  // cache policy bits of the weight tiles' LDS-direct loads (2, nontemporal, measured slower: config 4
-                  // layer prefill 0.44 -> 0.48 ms, config 3 1.30 -> 1.41 -- the tiles of an expert's row block are
-                  // re-read by each of its entry tiles, from L2)
+#define GG_WNT 0  // cache policy bits of the FP4 / Q8_0 weight tiles' LDS-direct loads (2, nontemporal, slower:
+                  // config 4 layer prefill 0.44 -> 0.48 ms -- the tiles of an expert's row block are re-read by each of
+                  // its entry tiles, from L2)
 #endif
 
 __device__ __forceinline__ void lds_load16(const void* g, void* lds_run) {
@@ -369,8 +370,8 @@ struct KSc {  // a lane's row scales for each 128-value half of a stage: its til
     uint4 h[KB / 4];
 };
 
-// Issue one stage's loads, all into registers: the wave's weight codes (12 bytes a lane per sub-block, one
-// contiguous 768-byte run per load) and rows' scales; and the activations of the wave's 16 entries 16 w + l % 16,
+// Issue one stage's loads, all into registers: the wave's weight codes (the stage-major tiles: three 16-byte chunks
+// a lane, each load one contiguous 1 KB run) and its rows' scale records; and the activations of the wave's 16 entries 16 w + l % 16,
 // lanes l / 16 reading consecutive 16-byte units of each entry's run of the stage, so that one load touches 16
 // entries' 64-byte pieces (a lane per entry, as the other kernels stage them, makes every load touch 64 rows):
 // unit c = 4 j + l / 16 of the stage (sub-block c / 2, 16-value half c % 2), the sums of 16 of sub-blocks
@@ -395,11 +396,8 @@ __device__ __forceinline__ void k_issue(int b0, uint4 (&wv)[3 * KB / 4], KSc<KB>
 
 // (v_fence: the value is taken as changed here, so that the compiler neither hoists the conversions that use it
 // above this point, next to the loads issued a stage earlier, nor waits for those loads before it)
-__device__ __forceinline__ void v_fence(uint32_t& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void v_fence(float& v) { asm volatile("" : "+v"(v)); }
-__device__ __forceinline__ void v_fence(uint2& v) { asm volatile("" : "+v"(v.x), "+v"(v.y)); }
 __device__ __forceinline__ void v_fence(int2& v) { asm volatile("" : "+v"(v.x), "+v"(v.y)); }
-__device__ __forceinline__ void v_fence(uint3& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z)); }
 __device__ __forceinline__ void v_fence(uint4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
 
 // The stage's activations into the FP16 operand runs (values 0..7 of a unit to the slot of (entry, K half 0) of its
