@@ -32,6 +32,11 @@ hipError_t moe_launch_grouped_swiglu(int type, const uint8_t* vg, const uint8_t*
                                      const int32_t* tile_e, const int32_t* tile_start, const int32_t* tile_n,
                                      const int32_t* in_rows, const int32_t* out_rows, int xt, const GShared* sh,
                                      hipStream_t stream);
+hipError_t moe_launch_grouped_gate_up(int type, const uint8_t* vg, const uint8_t* sg, const uint8_t* vu,
+                                      const uint8_t* su, long long vrb, long long srb, const qmatvec_q8* q, float* y,
+                                      int N, int K, int max_tiles, const int32_t* n_tiles, const int32_t* tile_e,
+                                      const int32_t* tile_start, const int32_t* tile_n, const int32_t* in_rows,
+                                      const int32_t* out_rows, hipStream_t stream);
 hipError_t moe_launch_dense_mfma(int type, const uint8_t* v, const uint8_t* s, long long vrb, long long srb,
                                  const qmatvec_q8* q, float* y, long long ldy, int N, int K, int T,
                                  hipStream_t stream);

@@ -432,7 +432,7 @@ __device__ __forceinline__ uint32_t sc_pair(uint32_t w, int j) {
 
 template <int NM, int KB, int NTU>
 __device__ __forceinline__ void k_compute(const KBuf<NM, KB>& B, const uint4 (&wv)[3 * KB / 4], const KSc<KB>& ks,
-                                          v16f (&acc)[NM][NTU], int l, int lr, int kh) {
+                                          v16f (&acc)[NTU], int l, int lr, int kh) {
     const v16f z = {};
     uint32_t wd[3 * KB];  // the lane's codes: 3 dwords (16 FP6 codes) per sub-block
 #pragma unroll
@@ -479,9 +479,9 @@ __device__ __forceinline__ void k_compute(const KBuf<NM, KB>& B, const uint4 (&w
             const float bdx = kh ? 0.0f : B.dx[32 * t + lr];
             const v16f S = __builtin_amdgcn_mfma_f32_32x32x2f32(aD, bdx, z, 0, 0, 0);
 #pragma unroll
-            for (int j = 0; j < 16; ++j) acc[0][t][j] = fmaf(P[j], S[j], acc[0][t][j]);
-            acc[0][t] = __builtin_amdgcn_mfma_f32_32x32x2f32(am0, bd[4 * hc + kh], acc[0][t], 0, 0, 0);
-            acc[0][t] = __builtin_amdgcn_mfma_f32_32x32x2f32(am1, bd[4 * hc + 2 + kh], acc[0][t], 0, 0, 0);
+            for (int j = 0; j < 16; ++j) acc[t][j] = fmaf(P[j], S[j], acc[t][j]);
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(am0, bd[4 * hc + kh], acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(am1, bd[4 * hc + 2 + kh], acc[t], 0, 0, 0);
         }
     }
 }
@@ -515,7 +515,8 @@ k_grouped(GArgs a) {
     // (or the dense rows' tiles), then the shared expert's. Each XCD takes one contiguous range of items (the
     // hardware deals workgroup i to XCD i % 8), so the consecutive tiles of one expert, which read the same
     // weight rows, run together on one XCD and share its L2 instead of fetching those rows once per XCD.
-    const int nrb = a.N / GG_ROWS;
+    // (the Q4_K gate / up launch, NM = 2: 64 rows of both matrices a workgroup, a matrix per pair of waves)
+    const int nrb = a.N / (TYPE == QT_Q4_K && NM == 2 ? GG_ROWS / 2 : GG_ROWS);
     const int nrt = a.n_tiles ? *a.n_tiles : (a.T + GG_TILE - 1) / GG_TILE;  // routed / dense tiles
     const int nsh = a.vs ? (a.sT + GG_TILE - 1) / GG_TILE : 0;
     const int items = (nrt + nsh) * nrb;
@@ -563,16 +564,19 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
     const int K = a.K, nb = K / 32;
     // the wave's 32-row group of the stacked matrix (the launcher requires N % 128 == 0 and K % 256 == 0) and
     // this lane's slots in its value and scale tiles (scale slots: 16 bytes per 8 blocks for Q8_0, 32 for FP4)
-    const int r0 = rb * GG_ROWS + 32 * w;
-    const long long grp = ((long long)e * a.N + r0) / 32;
     constexpr bool Q4K = TYPE == QT_Q4_K;
+    // Q4_K with NM = 2 (gate / up roles): waves 0, 1 take 32 gate rows each, waves 2, 3 the same rows of up
+    constexpr bool ROLE = Q4K && NM == 2;
+    const int r0 = ROLE ? rb * (GG_ROWS / 2) + 32 * (w & 1) : rb * GG_ROWS + 32 * w;
+    const long long grp = ((long long)e * a.N + r0) / 32;
     constexpr int SB = Q4K ? Q4K_TILE_SLOT : F16 ? 32 : 16;
     constexpr int VS = F16 && !Q4K ? 12 : 16;  // value slot bytes (Q4_K: a lane's 16-byte chunk of its stage)
     const uint8_t* vt[NM];
     const uint8_t* sct[NM];
-    vt[0] = (shk ? a.vs : a.v) + grp * a.vrb + VS * l;
-    sct[0] = (shk ? a.ss : a.s) + grp * a.srb + SB * lr;
-    if constexpr (NM == 2) {
+    const bool up_role = ROLE && w >= 2;
+    vt[0] = (shk ? a.vs : up_role ? a.v2 : a.v) + grp * a.vrb + VS * l;
+    sct[0] = (shk ? a.ss : up_role ? a.s2 : a.s) + grp * a.srb + SB * lr;
+    if constexpr (NM == 2 && !ROLE) {
         vt[1] = (shk ? a.vs2 : a.v2) + grp * a.vrb + VS * l;
         sct[1] = (shk ? a.ss2 : a.s2) + grp * a.srb + SB * lr;
     }
@@ -586,7 +590,6 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
         for (int t = 0; t < NTU; ++t) acc[m][t] = (v16f){};
     const int nst = nb / KB;
     if constexpr (Q4K) {
-        static_assert(NM == 1, "Q4_K: one matrix a launch (down's Q8_K input is quantized per 256 values)");
         // this lane's entry 16 w + l % 16 (the last one for lanes past the tile's entries) and unit l / 16
         const long long br = in_row(min(16 * w + (l & 15), cnt - 1));
         const int8_t* xu = a.xq + br * K + 16 * (l >> 4);
@@ -617,7 +620,7 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
             // (the last stage loads itself again, from L2: an unconditional issue keeps every stage's registers
             // in one place, where a skipped one would make the compiler copy them and wait for the loads)
             k_issue<KQ>(min(s + 1, ns - 1) * KQ, wvn, ksn, vt[0], sct[0], xu, xb, bsv, dxv, bsr, kdr);
-            k_compute<NM, KQ, NTU>(cur, wv, ks, acc, l, lr, kh);
+            k_compute<NM, KQ, NTU>(cur, wv, ks, acc[0], l, lr, kh);
             __builtin_amdgcn_sched_barrier(0);  // (the next stage's staging stays after this compute)
         };
         for (int s = 0; s < ns; s += 2) {
@@ -668,7 +671,25 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
         }
     }
     // acc[m][t][j] is C[row 8 (j / 4) + 4 kh + j % 4][entry 32 t + lr] of the wave's 32 x GG_TILE block
-    if constexpr (NM == 1) {
+    if constexpr (ROLE) {  // the gate waves hand g over through LDS (past the up waves' transpose areas); SwiGLU
+        static_assert(sizeof(buf) >= (4 * 32 * GG_TRS + 2 * GG_NT * 16 * 64) * sizeof(float), "g fits the buffer");
+        float* gx = (float*)&buf + 4 * 32 * GG_TRS + (w & 1) * (GG_NT * 16 * 64);
+        if (w < 2)
+#pragma unroll
+            for (int t = 0; t < NTU; ++t)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) gx[(t * 16 + j) * 64 + l] = acc[0][t][j];
+        __syncthreads();
+        if (w < 2) return;
+#pragma unroll
+        for (int t = 0; t < NTU; ++t)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {  // (the swiglu kernel's expression)
+                const float g = gx[(t * 16 + j) * 64 + l];
+                acc[0][t][j] = g / (1.0f + __expf(-g)) * acc[0][t][j];
+            }
+    }
+    if constexpr (NM == 1 || ROLE) {
         if (((uintptr_t)a.y | (uintptr_t)(a.ldy * 4)) & 15) {  // (uniform) rows not 16-byte aligned: 4-byte stores
 #pragma unroll
             for (int t = 0; t < NTU; ++t)
@@ -812,6 +833,22 @@ hipError_t moe_launch_grouped_swiglu(int type, const uint8_t* vg, const uint8_t*
     case QT_ROCMFP4_FAST: return launch_kernel(k_grouped<QT_ROCMFP4_FAST, 2, GG_KB2>, g, b, 0, stream, a);
     }
     return hipErrorInvalidDeviceFunction;
+}
+
+// Q4_K gate and up of the same tiles in one launch (64 rows of each matrix a workgroup: its gate waves hand g to its
+// up waves), then SwiGLU: y rows of N fp32 values (out_rows) of SiLU(g) u, the same bits as the two one-matrix
+// launches and the swiglu kernel; the caller quantizes them to down's Q8_K input (one scale per 256 values, which a
+// workgroup's rows cannot form)
+hipError_t moe_launch_grouped_gate_up(int type, const uint8_t* vg, const uint8_t* sg, const uint8_t* vu,
+                                      const uint8_t* su, long long vrb, long long srb, const qmatvec_q8* q, float* y,
+                                      int N, int K, int max_tiles, const int32_t* n_tiles, const int32_t* tile_e,
+                                      const int32_t* tile_start, const int32_t* tile_n, const int32_t* in_rows,
+                                      const int32_t* out_rows, hipStream_t stream) {
+    if (type != QT_Q4_K) return hipErrorInvalidValue;
+    GArgs a = {vg,         sg,     vrb,     srb,      q->q0, q->d0, y,  N,       K,       n_tiles, tile_e,
+               tile_start, tile_n, in_rows, out_rows, N,     0,     vu, su, nullptr, nullptr, 0};
+    bind_q8k(a, q);
+    return launch_kernel(k_grouped<QT_Q4_K, 2, GG_KB>, grid_of(2 * N, max_tiles), dim3(256), 0, stream, a);
 }
 
 // Dense: y[t][0..N) (row stride ldy) = W . x_t for t < T, every token a tile entry of the one matrix

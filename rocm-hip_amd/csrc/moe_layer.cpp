@@ -238,7 +238,17 @@ static hipError_t layer_forward(const moe_layer_desc* d, const float* x, const f
                 shared_done = true;
             }
         } else {
-            if (pm & 2) {
+            // Q4_K: gate, up and SwiGLU in one MFMA launch when both matrices have tiles and the tiles are mostly
+            // full (the per-entry kernel's condition in qmatvec_launch_q8_id_batch), then down's Q8_K input
+            const bool q4k_fused = (pm & 2) && mode && type == 12 && p.tile == moe_grouped_mfma_tile() &&
+                                   moe_grouped_mfma_ok(type, FE, E) && 4ll * p.max_tiles >= 3ll * NE &&
+                                   moe_packed_tiles(d->w_gate, type, E, rb_in, &vg, &sgp, &gvs, &gss) &&
+                                   moe_packed_tiles(d->w_up, type, E, rb_in, &vu, &sup, &gvs, &gss);
+            if (q4k_fused) {
+                CHECK(moe_launch_grouped_gate_up(type, vg, sgp, vu, sup, gvs, gss, &qx, g, FE, E, p.max_tiles, ntile,
+                                                 te, ts, tn, tok, pair, st));
+                CHECK(moe_quantize_q8k(g, T * NU * FE, &qa, st));
+            } else if (pm & 2) {
                 CHECK(qmatvec_launch_q8_id_batch(type, d->w_gate, rb_in, &qx, g, FE, E, p.max_tiles, p.tile, ntile,
                                                  te, ts, tn, tok, pair, st));
                 CHECK(qmatvec_launch_q8_id_batch(type, d->w_up, rb_in, &qx, u, FE, E, p.max_tiles, p.tile, ntile, te,
