@@ -192,6 +192,18 @@ struct BufOf<QT_ROCMFP4_FAST, NM, KB> {
     typedef HBuf<NM, KB> type;
 };
 
+#ifndef GG_ROLE
+#define GG_ROLE 0  // 1: the Q8_0 / FP4 gate / up launches also with a matrix per pair of waves (Q4_K always; for
+                   // Q8_0 / FP4 measured slower, their stage then serving half the rows: config 2 gate / up
+                   // 251 -> 265 us, config 4 219 -> 236, at occupancy 4 instead of 3)
+#endif
+// NM = 2 as roles: a workgroup takes 64 rows of both matrices, waves 0, 1 gate, 2, 3 up (one matrix per wave)
+template <int TYPE, int NM>
+struct Roles {
+    static constexpr bool on = NM == 2 && (TYPE == QT_Q4_K || GG_ROLE);
+    static constexpr int per_wave = on ? 1 : NM;  // matrices per wave
+};
+
 // ------------------------------------------------------------------ Q8_0: int8 MFMA
 
 // Issue one stage's loads. Wave w loads the activations of entry tile w % GG_NT, blocks w / GG_NT, + 4 / GG_NT, ...
@@ -489,8 +501,9 @@ __device__ __forceinline__ void k_compute(const KBuf<NM, KB>& B, const uint4 (&w
 // ------------------------------------------------------------------ the kernel
 
 template <int TYPE, int NM, int KB, int NTU>
-__device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE, NM, KB>::type& buf, int k, int rb,
-                                             int e, int st, int cnt, bool shk);
+__device__ __forceinline__ void grouped_tile(const GArgs& a,
+                                             typename BufOf<TYPE, Roles<TYPE, NM>::per_wave, KB>::type& buf, int k,
+                                             int rb, int e, int st, int cnt, bool shk);
 
 // NM = 1: y rows (fp32) of one matrix. NM = 2, SwiGLU: gate (a.v) and up (a.v2) rows of the same block, then
 // act = SiLU(g) u (the swiglu kernel's expression) and its Q8_0 blocks -- a wave's 32 rows of one entry are one
@@ -510,13 +523,13 @@ __global__ void __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(TYPE == QT_Q8_0 && NM == 1 ? GG_WPE_D8 : TYPE == QT_Q4_K ? GG_WPE_Q4K : GG_WPE)))
 #endif
 k_grouped(GArgs a) {
-    __shared__ __attribute__((aligned(1024))) typename BufOf<TYPE, NM, KB>::type buf;
+    __shared__ __attribute__((aligned(1024))) typename BufOf<TYPE, Roles<TYPE, NM>::per_wave, KB>::type buf;
     // Work items (tile, 128-row block), tile-major, over the tiles that exist: the routed tiles 0 .. n_tiles - 1
     // (or the dense rows' tiles), then the shared expert's. Each XCD takes one contiguous range of items (the
     // hardware deals workgroup i to XCD i % 8), so the consecutive tiles of one expert, which read the same
     // weight rows, run together on one XCD and share its L2 instead of fetching those rows once per XCD.
-    // (the Q4_K gate / up launch, NM = 2: 64 rows of both matrices a workgroup, a matrix per pair of waves)
-    const int nrb = a.N / (TYPE == QT_Q4_K && NM == 2 ? GG_ROWS / 2 : GG_ROWS);
+    // (NM = 2 as roles: 64 rows of both matrices a workgroup, a matrix per pair of waves)
+    const int nrb = a.N / (Roles<TYPE, NM>::on ? GG_ROWS / 2 : GG_ROWS);
     const int nrt = a.n_tiles ? *a.n_tiles : (a.T + GG_TILE - 1) / GG_TILE;  // routed / dense tiles
     const int nsh = a.vs ? (a.sT + GG_TILE - 1) / GG_TILE : 0;
     const int items = (nrt + nsh) * nrb;
@@ -555,8 +568,9 @@ k_grouped(GArgs a) {
 // One workgroup's tile k (expert e, entries st .. st + cnt - 1) and row block rb, with NTU of its GG_NT 32-entry
 // MFMA tiles in use
 template <int TYPE, int NM, int KB, int NTU>
-__device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE, NM, KB>::type& buf, int k, int rb,
-                                             int e, int st, int cnt, bool shk) {
+__device__ __forceinline__ void grouped_tile(const GArgs& a,
+                                             typename BufOf<TYPE, Roles<TYPE, NM>::per_wave, KB>::type& buf, int k,
+                                             int rb, int e, int st, int cnt, bool shk) {
     constexpr bool F16 = TYPE != QT_Q8_0;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lr = l & 31, kh = l >> 5;
     auto in_row = [&](int i) { return !shk && a.in_rows ? a.in_rows[st + i] : st + i; };
@@ -565,17 +579,18 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
     // the wave's 32-row group of the stacked matrix (the launcher requires N % 128 == 0 and K % 256 == 0) and
     // this lane's slots in its value and scale tiles (scale slots: 16 bytes per 8 blocks for Q8_0, 32 for FP4)
     constexpr bool Q4K = TYPE == QT_Q4_K;
-    // Q4_K with NM = 2 (gate / up roles): waves 0, 1 take 32 gate rows each, waves 2, 3 the same rows of up
-    constexpr bool ROLE = Q4K && NM == 2;
+    // NM = 2 as roles: waves 0, 1 take 32 gate rows each, waves 2, 3 the same rows of up
+    constexpr bool ROLE = Roles<TYPE, NM>::on;
+    constexpr int NMW = Roles<TYPE, NM>::per_wave;
     const int r0 = ROLE ? rb * (GG_ROWS / 2) + 32 * (w & 1) : rb * GG_ROWS + 32 * w;
     const long long grp = ((long long)e * a.N + r0) / 32;
     constexpr int SB = Q4K ? Q4K_TILE_SLOT : F16 ? 32 : 16;
     constexpr int VS = F16 && !Q4K ? 12 : 16;  // value slot bytes (Q4_K: a lane's 16-byte chunk of its stage)
-    const uint8_t* vt[NM];
-    const uint8_t* sct[NM];
+    const uint8_t* vt[NMW];
+    const uint8_t* sct[NMW];
     const bool up_role = ROLE && w >= 2;
-    vt[0] = (shk ? a.vs : up_role ? a.v2 : a.v) + grp * a.vrb + VS * l;
-    sct[0] = (shk ? a.ss : up_role ? a.s2 : a.s) + grp * a.srb + SB * lr;
+    vt[0] = (shk ? (up_role ? a.vs2 : a.vs) : up_role ? a.v2 : a.v) + grp * a.vrb + VS * l;
+    sct[0] = (shk ? (up_role ? a.ss2 : a.ss) : up_role ? a.s2 : a.s) + grp * a.srb + SB * lr;
     if constexpr (NM == 2 && !ROLE) {
         vt[1] = (shk ? a.vs2 : a.v2) + grp * a.vrb + VS * l;
         sct[1] = (shk ? a.ss2 : a.s2) + grp * a.srb + SB * lr;
@@ -583,9 +598,9 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
     const int de = min(GG_TILE / 4 * w + (l & (GG_TILE / 4 - 1)), cnt - 1);  // the entry whose scales this lane loads
     const float* dxr = a.xd + ((a.xt & GX_IN) ? (long long)k * GG_TILE + de : (long long)in_row(de)) * nb;
 
-    v16f acc[NM][NTU];
+    v16f acc[NMW][NTU];
 #pragma unroll
-    for (int m = 0; m < NM; ++m)
+    for (int m = 0; m < NMW; ++m)
 #pragma unroll
         for (int t = 0; t < NTU; ++t) acc[m][t] = (v16f){};
     const int nst = nb / KB;
@@ -605,8 +620,8 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
         float dxv;
         const int ns = nb / KQ;
         k_issue<KQ>(0, wvn, ksn, vt[0], sct[0], xu, xb, bsv, dxv, bsr, kdr);
-        auto step = [&](KBuf<NM, KQ>& cur, int s) {
-            k_stage<NM, KQ>(cur, xb, bsv, dxv, w, l);
+        auto step = [&](KBuf<NMW, KQ>& cur, int s) {
+            k_stage<NMW, KQ>(cur, xb, bsv, dxv, w, l);
             KSc<KQ> ks = ksn;
             uint4 wv[3 * KQ / 4];
 #pragma unroll
@@ -620,7 +635,7 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
             // (the last stage loads itself again, from L2: an unconditional issue keeps every stage's registers
             // in one place, where a skipped one would make the compiler copy them and wait for the loads)
             k_issue<KQ>(min(s + 1, ns - 1) * KQ, wvn, ksn, vt[0], sct[0], xu, xb, bsv, dxv, bsr, kdr);
-            k_compute<NM, KQ, NTU>(cur, wv, ks, acc[0], l, lr, kh);
+            k_compute<NMW, KQ, NTU>(cur, wv, ks, acc[0], l, lr, kh);
             __builtin_amdgcn_sched_barrier(0);  // (the next stage's staging stays after this compute)
         };
         for (int s = 0; s < ns; s += 2) {
@@ -639,12 +654,12 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
             xrow = a.xq + (long long)in_row(min(32 * (w % GG_NT) + lr, cnt - 1)) * K + 16 * kh;
             xs = 32;
         }
-        uint4 wsc[NM];
+        uint4 wsc[NMW];
         for (int s = 0; s < nst; ++s) {
-            q_issue<NM, KB>(buf, s * KB, wsc, vt, sct, xrow, xs, dxr, w, l);
+            q_issue<NMW, KB>(buf, s * KB, wsc, vt, sct, xrow, xs, dxr, w, l);
             wait_vm<0>();
             __syncthreads();
-            q_compute<NM, KB, NTU>(buf, wsc, acc, w, l, lr, kh);
+            q_compute<NMW, KB, NTU>(buf, wsc, acc, w, l, lr, kh);
             __syncthreads();
         }
     } else {
@@ -659,21 +674,23 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
             xu = a.xq + (long long)in_row(min(ue, cnt - 1)) * K + 16 * uh;
             xs = 32;
         }
-        uint4 wsc[NM][KB / 4];
+        uint4 wsc[NMW][KB / 4];
         uint4 xb[KB / 2];
         for (int s = 0; s < nst; ++s) {
-            h_issue<NM, KB>(buf, s * KB, wsc, vt, sct, xu, xs, xb, dxr, w, l, tid);
+            h_issue<NMW, KB>(buf, s * KB, wsc, vt, sct, xu, xs, xb, dxr, w, l, tid);
             wait_vm<0>();
-            h_stage_b<NM, KB>(buf, xb, tid);
+            h_stage_b<NMW, KB>(buf, xb, tid);
             __syncthreads();
-            h_compute<NM, KB, NTU>(buf, wsc, acc, w, l, lr);
+            h_compute<NMW, KB, NTU>(buf, wsc, acc, w, l, lr);
             __syncthreads();
         }
     }
     // acc[m][t][j] is C[row 8 (j / 4) + 4 kh + j % 4][entry 32 t + lr] of the wave's 32 x GG_TILE block
-    if constexpr (ROLE) {  // the gate waves hand g over through LDS (past the up waves' transpose areas); SwiGLU
-        static_assert(sizeof(buf) >= (4 * 32 * GG_TRS + 2 * GG_NT * 16 * 64) * sizeof(float), "g fits the buffer");
-        float* gx = (float*)&buf + 4 * 32 * GG_TRS + (w & 1) * (GG_NT * 16 * 64);
+    // ROLE: the gate waves hand g over through LDS (Q4_K: past the up waves' transpose areas) and leave
+    constexpr int GX0 = Q4K ? 4 * 32 * GG_TRS : 0;
+    static_assert(!ROLE || sizeof(buf) >= (GX0 + 2 * GG_NT * 16 * 64) * sizeof(float), "g fits the buffer");
+    float* gx = (float*)&buf + GX0 + (w & 1) * (GG_NT * 16 * 64);
+    if constexpr (ROLE) {
         if (w < 2)
 #pragma unroll
             for (int t = 0; t < NTU; ++t)
@@ -681,15 +698,20 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
                 for (int j = 0; j < 16; ++j) gx[(t * 16 + j) * 64 + l] = acc[0][t][j];
         __syncthreads();
         if (w < 2) return;
+    }
+    // gate and up of output j of tile t (the two matrices of a wave, or g from LDS and the wave's up)
+    auto gate_of = [&](int t, int j) { return ROLE ? gx[(t * 16 + j) * 64 + l] : acc[0][t][j]; };
+    auto up_of = [&](int t, int j) { return acc[NMW - 1][t][j]; };
+    if constexpr (ROLE && Q4K) {  // SwiGLU (the swiglu kernel's expression), stored as fp32 rows below
 #pragma unroll
         for (int t = 0; t < NTU; ++t)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {  // (the swiglu kernel's expression)
-                const float g = gx[(t * 16 + j) * 64 + l];
-                acc[0][t][j] = g / (1.0f + __expf(-g)) * acc[0][t][j];
+            for (int j = 0; j < 16; ++j) {
+                const float g = gate_of(t, j);
+                acc[0][t][j] = g / (1.0f + __expf(-g)) * up_of(t, j);
             }
     }
-    if constexpr (NM == 1 || ROLE) {
+    if constexpr (NM == 1 || (ROLE && Q4K)) {
         if (((uintptr_t)a.y | (uintptr_t)(a.ldy * 4)) & 15) {  // (uniform) rows not 16-byte aligned: 4-byte stores
 #pragma unroll
             for (int t = 0; t < NTU; ++t)
@@ -728,8 +750,8 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a, typename BufOf<TYPE
             float am = 0.0f;
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                const float g = acc[0][t][j];
-                act[j] = g / (1.0f + __expf(-g)) * acc[1][t][j];
+                const float g = gate_of(t, j);
+                act[j] = g / (1.0f + __expf(-g)) * up_of(t, j);
                 am = fmaxf(am, fabsf(act[j]));
             }
             am = fmaxf(am, __shfl_xor(am, 32, 64));  // the block's other 16 rows
@@ -826,7 +848,7 @@ hipError_t moe_launch_grouped_swiglu(int type, const uint8_t* vg, const uint8_t*
                tile_start, tile_n, in_rows, out_rows, N,     0,     vu,      su, aq, ad, xt};
     int tiles = max_tiles;
     bind_shared(a, sh, max_tiles, tiles);
-    const dim3 g = grid_of(N, tiles), b(256);
+    const dim3 g = grid_of(GG_ROLE ? 2 * N : N, tiles), b(256);  // (roles: 64-row blocks)
     switch (type) {
     case QT_Q8_0: return launch_kernel(k_grouped<QT_Q8_0, 2, GG_KB2>, g, b, 0, stream, a);
     case QT_ROCMFP4: return launch_kernel(k_grouped<QT_ROCMFP4, 2, GG_KB2>, g, b, 0, stream, a);
