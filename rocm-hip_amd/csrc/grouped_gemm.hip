@@ -292,13 +292,13 @@ __device__ __forceinline__ v8h scaled8(const v32h& d, int q, uint32_t sc) {
     return r;
 }
 
-// Issue one stage: weight tiles and activation scales to LDS, this thread's activation units to registers. Unit
-// (entry tid % 64, half (tid / 64) % 2, block tid / 128 + 2 j): the 16 int8 values 16 h .. of the entry's block.
+// Issue one stage: weight tiles and activation scales to LDS, this thread's activation units to registers: unit j
+// at xu + xs b0 + xj j (h_unit gives the entry, block and half each one holds).
 template <int NM, int KB>
 __device__ __forceinline__ void h_issue(HBuf<NM, KB>& B, int b0, uint4 (&wsc)[NM][KB / 4],
                                         const uint8_t* const (&vt)[NM], const uint8_t* const (&st)[NM],
-                                        const int8_t* xu, int xs, uint4 (&xb)[KB / 2], const float* dxr, int w,
-                                        int l, int tid) {
+                                        const int8_t* xu, int xs, int xj, uint4 (&xb)[KB / 2], const float* dxr,
+                                        int w, int l) {
     constexpr int ES = GG_TILE / 4;
 #pragma unroll
     for (int m = 0; m < NM; ++m)
@@ -309,21 +309,33 @@ __device__ __forceinline__ void h_issue(HBuf<NM, KB>& B, int b0, uint4 (&wsc)[NM
     for (int q = 0; q < KB / 4; ++q)
         if (l < ES) lds_load16(dxr + b0 + 4 * q, &B.dx[q][ES * w][0]);
 #pragma unroll
-    for (int j = 0; j < KB / 2; ++j) xb[j] = *(const uint4*)(xu + xs * (b0 + (tid >> 7) + 2 * j));
+    for (int j = 0; j < KB / 2; ++j) xb[j] = *(const uint4*)(xu + xs * b0 + xj * j);
 #pragma unroll
     for (int m = 0; m < NM; ++m)  // 4 blocks' (e0, e1) FP16 pairs per 16 bytes of the row's 32-byte slot
 #pragma unroll
         for (int q = 0; q < KB / 4; ++q) wsc[m][q] = *(const uint4*)(st[m] + 1024 * (b0 >> 3) + 16 * (((b0 >> 2) + q) & 1));
 }
 
+// Activation unit j of this thread (16 int8 values: half h of block bb of the stage, for entry e). Entry-tile
+// order (rows = false, contiguous 1 KB runs): entry tid % 64, half (tid / 64) % 2, block tid / 128 + 2 j.
+// Gathered rows (rows = true): the wave's 16 entries 16 w + l % 16, four lanes each on consecutive 16-byte pieces
+// of the entry's run of the stage (unit c = 4 j + l / 16: block c / 2, half c % 2), so that a load touches 16 rows'
+// 64-byte pieces instead of 64 rows' 16-byte ones.
+__device__ __forceinline__ void h_unit(bool rows, int j, int tid, int& e, int& bb, int& h) {
+    const int w = tid >> 6, l = tid & 63, c = 4 * j + (l >> 4);
+    e = rows ? 16 * w + (l & 15) : tid & 63;
+    bb = rows ? c >> 1 : (tid >> 7) + 2 * j;
+    h = rows ? c & 1 : (tid >> 6) & 1;
+}
+
 // This thread's activation units, converted, into the FP16 operand runs: values 0..7 of a unit to the slot of
 // (entry, K half 0) of its MFMA half, values 8..15 to that of (entry, K half 1)
 template <int NM, int KB, typename Buf = HBuf<NM, KB>>
-__device__ __forceinline__ void h_stage_b(Buf& B, const uint4 (&xb)[KB / 2], int tid) {
-    const int e = tid & 63, h = (tid >> 6) & 1;
+__device__ __forceinline__ void h_stage_b(Buf& B, const uint4 (&xb)[KB / 2], bool rows, int tid) {
 #pragma unroll
     for (int j = 0; j < KB / 2; ++j) {
-        const int bb = (tid >> 7) + 2 * j;
+        int e, bb, h;
+        h_unit(rows, j, tid, e, bb, h);
         uint8_t* run = B.b[bb][e >> 5][h];
         *(uint4*)(run + 16 * (e & 31)) = i8x8_to_f16(xb[j].x, xb[j].y);
         *(uint4*)(run + 16 * (32 + (e & 31))) = i8x8_to_f16(xb[j].z, xb[j].w);
@@ -663,23 +675,28 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a,
             __syncthreads();
         }
     } else {
-        // this thread's activation unit: entry tid % 64, 16-value half (tid / 64) % 2
-        const int ue = tid & 63, uh = (tid >> 6) & 1;
+        // this thread's activation units (h_unit)
+        const bool rows = !(a.xt & GX_IN);
+        int ue, ub, uh;
+        h_unit(rows, 0, tid, ue, ub, uh);
         const int8_t* xu;
-        int xs;
-        if (a.xt & GX_IN) {
-            xu = a.xq + ((long long)k * nb * GG_NT + (ue >> 5)) * 1024 + 16 * (32 * uh + (ue & 31));
+        int xs, xj;
+        if (!rows) {  // unit j: block ub + 2 j
+            xu = a.xq + ((long long)k * nb * GG_NT + (ue >> 5)) * 1024 + 16 * (32 * uh + (ue & 31)) +
+                 (long long)GG_NT * 1024 * ub;
             xs = GG_NT * 1024;
-        } else {
-            xu = a.xq + (long long)in_row(min(ue, cnt - 1)) * K + 16 * uh;
+            xj = 2 * GG_NT * 1024;
+        } else {  // unit j: byte 64 j + 16 (l / 16) of the entry's 128-byte run of the stage
+            xu = a.xq + (long long)in_row(min(ue, cnt - 1)) * K + 16 * (l >> 4);
             xs = 32;
+            xj = 64;
         }
         uint4 wsc[NMW][KB / 4];
         uint4 xb[KB / 2];
         for (int s = 0; s < nst; ++s) {
-            h_issue<NMW, KB>(buf, s * KB, wsc, vt, sct, xu, xs, xb, dxr, w, l, tid);
+            h_issue<NMW, KB>(buf, s * KB, wsc, vt, sct, xu, xs, xj, xb, dxr, w, l);
             wait_vm<0>();
-            h_stage_b<NMW, KB>(buf, xb, tid);
+            h_stage_b<NMW, KB>(buf, xb, rows, tid);
             __syncthreads();
             h_compute<NMW, KB, NTU>(buf, wsc, acc, w, l, lr);
             __syncthreads();
