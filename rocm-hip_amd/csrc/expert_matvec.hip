@@ -177,10 +177,10 @@ __global__ void __launch_bounds__(256) k_pack(const uint8_t* W, long long row_by
 // b, one run of 64 lane slots, slot l for row 32 g + l % 32 and K half h = l / 32:
 //   Q8_0:      16-byte slots: the block's int8 values 16 h .. 16 h + 15 (the int8 MFMA's A);
 //   FP4 types: 12-byte slots: the block's values 8 h .. 8 h + 7, then 16 + 8 h .. + 7 (the f16 MFMAs' A of each
-//              16-value half), each as the FP6 E2M3 code of codebook value / 2, 6 bits per value from bit 0 up.
-//   Q4_K:      the same 12-byte slots per 32-value sub-block, each code the FP6 E2M3 of quant / 2 (quant 0..15),
-//              stage-major: the four slots of a lane for sub-blocks 4 s .. 4 s + 3 as 48 contiguous bytes, split in
-//              three 16-byte chunks, chunk i at 1024 i + 16 l of the stage's 3 KB (three coalesced loads a stage).
+//              16-value half), each as the FP6 E2M3 code of codebook value / 2, 6 bits per value from bit 0 up;
+//   Q4_K:      the same 12-byte slots per 32-value sub-block, each code the FP6 E2M3 of quant / 2 (quant 0..15);
+//              both stage-major: the four slots of a lane for blocks 4 s .. 4 s + 3 as 48 contiguous bytes, split
+//              in three 16-byte chunks, chunk i at 1024 i + 16 l of the stage's 3 KB (three coalesced loads a stage).
 // Scale tiles, per group g and 8-block group q (Q4_K: super-block), 32 row slots: Q8_0 16 bytes (8 blocks' FP16 d);
 // FP4 types 32 bytes (per block the FP16 pair (e0, e1) of its UE4M3 half-scales, FAST (e, e)); Q4_K 32 bytes, 16
 // per 128-value half c: the sub-block scales sc_4c..sc_4c+3 and mins m_4c..m_4c+3 as bytes, the FP16 d and dmin,
@@ -222,7 +222,7 @@ __global__ void __launch_bounds__(256) k_pack_tiles(const uint8_t* W, long long 
         // the native block holding block b (Q4_K: super-block b / 8, of which b is sub-block b % 8)
         const uint8_t* blk = W + (32 * g + (l & 31)) * row_bytes + (long long)(TYPE == QT_Q4_K ? b >> 3 : b) * BB;
         uint8_t* dst = V + SS * i;
-        if constexpr (TYPE == QT_Q4_K)  // stage-major: byte p of the lane's 48 for the stage (4 sub-blocks)
+        if constexpr (TYPE != QT_Q8_0)  // stage-major: byte p of the lane's 48 for the stage (4 blocks)
             dst = V + (long long)g * nb * 768 + 3072 * (b >> 2) + 16 * l;
         if constexpr (TYPE == QT_Q8_0) {
             for (int j = 0; j < 16; ++j) dst[j] = blk[2 + 16 * h + j];
@@ -240,8 +240,8 @@ __global__ void __launch_bounds__(256) k_pack_tiles(const uint8_t* W, long long 
                 if ((bit & 31) > 26) w[(bit >> 5) + 1] |= f >> (32 - (bit & 31));
             }
             for (int j = 0; j < 12; ++j) {
-                const int p = TYPE == QT_Q4_K ? 12 * (b & 3) + j : j;
-                dst[TYPE == QT_Q4_K ? 1024 * (p >> 4) + (p & 15) : j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+                const int p = 12 * (b & 3) + j;
+                dst[1024 * (p >> 4) + (p & 15)] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
             }
         }
         return;

@@ -48,8 +48,8 @@ __host__ __device__ constexpr int fmt_scale_row(int type, int K) { return type =
 // which the hardware decodes 32 at a time). Scales: Q8_0 its FP16 d (2 per block); the FP4 types each block's
 // (e0, e1) UE4M3 half-scales decoded to an FP16 pair (FAST: (e, e)), 4 per block; Q4_K per super-block of 256 a
 // 32-byte slot (Q4K_TILE_SLOT), 16 bytes per 128-value half: its four 6-bit sub-block scales and four mins as
-// bytes, then the super-block's FP16 d and dmin, 4 bytes of zeros (one 16-byte load a lane and half). The Q4_K
-// value tiles are stage-major: the 48 bytes of a lane's codes for four consecutive sub-blocks in three 16-byte
+// bytes, then the super-block's FP16 d and dmin, 4 bytes of zeros (one 16-byte load a lane and half). The FP4 and
+// Q4_K value tiles are stage-major: the 48 bytes of a lane's codes for four consecutive blocks in three 16-byte
 // chunks, chunk i of the stage at 1024 i + 16 lane.
 #define Q4K_TILE_SLOT 32
 __host__ __device__ constexpr int tile_value_row(int type, int K) { return type == QT_Q8_0 ? K : K / 4 * 3; }

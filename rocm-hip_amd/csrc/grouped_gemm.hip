@@ -133,10 +133,6 @@ typedef __attribute__((address_space(3))) void lds_void;
 __device__ __forceinline__ void lds_load16(const void* g, void* lds_run) {
     __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_run, 16, 0, 0);
 }
-// 12 bytes a lane: they land in 16-byte LDS slots (lane l at 16 l)
-__device__ __forceinline__ void lds_load12(const void* g, void* lds_run) {
-    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_run, 12, 0, GG_WNT);
-}
 // The weight tiles' 16-byte loads (the cache policy GG_WNT)
 __device__ __forceinline__ void lds_load16w(const void* g, void* lds_run) {
     __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_run, 16, 0, GG_WNT);
@@ -157,7 +153,7 @@ struct GBuf {  // Q8_0
 };
 template <int NM, int KB>
 struct HBuf {  // FP4 types
-    uint8_t a[NM][4][KB][1024];      // [matrix][wave][block][lane * 16]: 12-byte FP6 slots
+    uint8_t a[NM][4][3 * KB / 4][1024];  // [matrix][wave][chunk][lane * 16]: the stage-major tiles' 16-byte chunks
     uint8_t b[KB][GG_NT][2][1024];   // [block][entry tile][16-value half][lane * 16]: FP16 activations
     float dx[KB / 4][GG_TILE][4];
 };
@@ -303,8 +299,8 @@ __device__ __forceinline__ void h_issue(HBuf<NM, KB>& B, int b0, uint4 (&wsc)[NM
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int c = 0; c < KB; ++c)  // 768-byte runs, 12 bytes a lane, landing in 16-byte LDS slots
-            lds_load12(vt[m] + 768 * (b0 + c), B.a[m][w][c]);
+        for (int c = 0; c < 3 * KB / 4; ++c)  // the stage's 1 KB chunks of the wave's codes
+            lds_load16w(vt[m] + 768 * b0 + 1024 * c, B.a[m][w][c]);
 #pragma unroll
     for (int q = 0; q < KB / 4; ++q)
         if (l < ES) lds_load16(dxr + b0 + 4 * q, &B.dx[q][ES * w][0]);
@@ -350,10 +346,12 @@ __device__ __forceinline__ void h_compute(const HBuf<NM, KB>& B, const uint4 (&w
     for (int bp = 0; bp < KB; bp += 2) {  // a block pair: 32 FP6 codes a lane, one conversion
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
-            const uint3 c0 = *(const uint3*)(B.a[m][w][bp] + 16 * l);
-            const uint3 c1 = *(const uint3*)(B.a[m][w][bp + 1] + 16 * l);
-            const v32h d =
-                __builtin_amdgcn_cvt_scalef32_pk32_f16_fp6((v6u){c0.x, c0.y, c0.z, c1.x, c1.y, c1.z}, 2.0f);
+            // blocks bp, bp + 1 of a stage of four: the lane's dwords 3 (bp % 4) .. + 5 of its 12, in chunks
+            // 3 (bp / 4) + (bp % 4) / 2 and the next
+            const int ch = 3 * (bp >> 2) + ((bp & 3) >> 1);
+            const uint4 q0 = *(const uint4*)(B.a[m][w][ch] + 16 * l), q1 = *(const uint4*)(B.a[m][w][ch + 1] + 16 * l);
+            const v6u c6 = (bp & 2) ? (v6u){q0.z, q0.w, q1.x, q1.y, q1.z, q1.w} : (v6u){q0.x, q0.y, q0.z, q0.w, q1.x, q1.y};
+            const v32h d = __builtin_amdgcn_cvt_scalef32_pk32_f16_fp6(c6, 2.0f);
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 const int bb = bp + k;
@@ -597,7 +595,7 @@ __device__ __forceinline__ void grouped_tile(const GArgs& a,
     const int r0 = ROLE ? rb * (GG_ROWS / 2) + 32 * (w & 1) : rb * GG_ROWS + 32 * w;
     const long long grp = ((long long)e * a.N + r0) / 32;
     constexpr int SB = Q4K ? Q4K_TILE_SLOT : F16 ? 32 : 16;
-    constexpr int VS = F16 && !Q4K ? 12 : 16;  // value slot bytes (Q4_K: a lane's 16-byte chunk of its stage)
+    constexpr int VS = 16;  // value slot bytes (FP4, Q4_K: a lane's 16-byte chunk of its stage)
     const uint8_t* vt[NMW];
     const uint8_t* sct[NMW];
     const bool up_role = ROLE && w >= 2;
